@@ -1,0 +1,105 @@
+"""ctypes binding of libfdwt_hip.so (the C ABI declared in include/fdwt_hip.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (or ``csrc/build.py``) and loaded
+after torch, so that it binds to the HIP runtime torch already loaded.  There is no CPU
+fallback: every operator of this package raises if its inputs are not on a ROCm device or
+if the library is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfdwt_hip.so")
+_LOCK = threading.Lock()
+_LIB = None
+
+DTYPE = {torch.float32: 0, torch.float64: 1, torch.float16: 2, torch.bfloat16: 3}
+ERR_TOO_LONG = -2
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_PI64 = ctypes.POINTER(ctypes.c_int64)
+_PF32 = ctypes.POINTER(ctypes.c_float)
+
+# name -> argument types (restype int unless listed in _RESTYPE)
+SIGNATURES = {
+    "fdwt_error_string": [ctypes.c_int],
+    "fdwt_version": [],
+    "fdwt_dwt_analysis": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P],
+    "fdwt_dwt_synthesis": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P],
+    "fdwt_analysis_chain": [_P, _PP, _P, _P, _P, _I64, _PI64, _PI64, _I32, _I32, _I32, _I32,
+                            _I32, _P],
+    "fdwt_synthesis_chain": [_P, _PP, _P, _P, _P, _I64, _PI64, _PI64, _I32, _I32, _I32, _I32,
+                             _I32, _P],
+    "fdwt_chain_max_length": [_I32, _I32],
+}
+_RESTYPE = {"fdwt_error_string": ctypes.c_char_p, "fdwt_version": ctypes.c_char_p,
+            "fdwt_chain_max_length": ctypes.c_int64}
+
+
+def library_path() -> str:
+    return _PATH
+
+
+def lib():
+    """Load the HIP library (once)."""
+    global _LIB
+    if _LIB is None:
+        with _LOCK:
+            if _LIB is None:
+                if not os.path.exists(_PATH):
+                    raise RuntimeError(
+                        f"{_PATH} is missing: build the HIP kernels first "
+                        "(python -c 'import __graft_entry__ as g; g.build()')")
+                handle = ctypes.CDLL(_PATH)
+                for name, args in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.argtypes = args
+                    fn.restype = _RESTYPE.get(name, ctypes.c_int)
+                _LIB = handle
+    return _LIB
+
+
+def check(code: int, what: str = ""):
+    if code != 0:
+        msg = lib().fdwt_error_string(code).decode()
+        raise RuntimeError(f"{what}: {msg} (code {code})" if what else msg)
+
+
+def require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "pytorch_morlet_fdwt_amd runs its operators with HIP kernels on ROCm GPU "
+                f"tensors only; got a tensor on {t.device}")
+
+
+def stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def ptr_array(tensors):
+    return (ctypes.c_void_p * max(1, len(tensors)))(
+        *[0 if t is None else t.data_ptr() for t in tensors])
+
+
+def i64_array(values):
+    return (ctypes.c_int64 * max(1, len(values)))(*[int(v) for v in values])
+
+
+def dtype_code(dtype) -> int:
+    try:
+        return DTYPE[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}") from None

@@ -1,0 +1,773 @@
+// Mallat DWT kernels for gfx950: analysis (two bands, stride-2) and its exact transpose.
+//
+// Analysis of one level (reference semantics: src/fdwt/kernels/dwt.py:73-98):
+//     y_b[o] = sum_{j<L} h_b[j] x_ext[2 o + off - j]
+// Synthesis is the transpose: z[p] = sum_{2o + off - j = p} h0[j] a[o] + h1[j] d[o] for the
+// extended positions p, then every z[p] is folded back onto y[ext(p)] (dwt.py:101-175).
+//
+// Design (MI355X-first, not a translation of the Triton kernels):
+//  * Boundary extension is applied only when a signal is staged into LDS (or when its
+//    margins are filled); the tap loops read a branch-free, already extended window.
+//  * Each thread computes V consecutive outputs from a register window (2V + L - 2 samples
+//    for analysis, V + L/2 - 1 coefficients per band for synthesis); taps live in SGPRs.
+//  * Fused chains: one workgroup owns one row, and the low band of every level stays in LDS
+//    (ping-pong buffers), so the input is read once and each band is written once.
+//    Level 0 of an analysis chain streams x through an LDS window whose next chunk is
+//    prefetched into registers while the current chunk is computed.
+//  * Split kernels (one level, several workgroups per row) serve rows too long for LDS.
+#include <algorithm>
+
+#include "common.h"
+
+namespace fdwt {
+namespace {
+
+constexpr int NT = 256;          // threads per workgroup (4 wave64)
+constexpr int VA = 2;            // consecutive analysis outputs per thread
+constexpr int GA = 4;            // thread groups per analysis chunk
+constexpr int CO = NT * VA * GA; // outputs per analysis chunk (2048)
+constexpr int VS = 2;            // consecutive synthesis pairs (u values) per thread
+constexpr int MAXL_T = 32;       // largest templated filter length
+
+struct AChainArgs {
+  const void* x;
+  void* details[FDWT_MAX_LEVELS];
+  void* approx;
+  const void* h0;
+  const void* h1;
+  int32_t n_in[FDWT_MAX_LEVELS];
+  int32_t n_out[FDWT_MAX_LEVELS];
+  int32_t levels, taps, mode, off;
+  int32_t capA, capB;
+  int32_t split;  // chunks per workgroup in split mode (levels == 1), 0 = whole row
+};
+
+struct SChainArgs {
+  const void* approx;
+  const void* details[FDWT_MAX_LEVELS];
+  void* out;
+  const void* h0;
+  const void* h1;
+  int32_t nc[FDWT_MAX_LEVELS];
+  int32_t n_out[FDWT_MAX_LEVELS];
+  int32_t levels, taps, mode, off;
+  int32_t capA, capB, capE;
+  int32_t split;  // output positions per workgroup in split mode (levels == 1), 0 = row
+};
+
+// ------------------------------------------------------------------ compute windows
+template <typename T, int LT>
+__device__ inline void analysis_pair(const T* __restrict__ s, const T* hr0, const T* hr1,
+                                     int L, T (&y0)[VA], T (&y1)[VA]) {
+  if constexpr (LT > 0) {
+    constexpr int W = 2 * VA + LT - 2;
+    T w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = s[k];
+#pragma unroll
+    for (int q = 0; q < VA; ++q) {
+      T a0 = T(0), a1 = T(0);
+#pragma unroll
+      for (int i = 0; i < LT; ++i) {
+        a0 = fma(hr0[i], w[2 * q + i], a0);
+        a1 = fma(hr1[i], w[2 * q + i], a1);
+      }
+      y0[q] = a0;
+      y1[q] = a1;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < VA; ++q) {
+      T a0 = T(0), a1 = T(0);
+      for (int i = 0; i < L; ++i) {
+        const T v = s[2 * q + i];
+        a0 = fma(hr0[i], v, a0);
+        a1 = fma(hr1[i], v, a1);
+      }
+      y0[q] = a0;
+      y1[q] = a1;
+    }
+  }
+}
+
+// z_odd[q] (position off + 2(u0+q) - 1) and z_even[q] (position off + 2(u0+q)) from the
+// low band a[u0 ..] (LDS, zero margins) and the high band d[u0 ..] (global, bounds checked).
+template <typename S, typename T, int LT>
+__device__ inline void synthesis_pair(const T* __restrict__ a, const S* __restrict__ drow,
+                                      int u0, int nc, const T* h0, const T* h1, int L,
+                                      T (&zo)[VS], T (&ze)[VS]) {
+  if constexpr (LT > 0) {
+    constexpr int H = LT / 2;
+    constexpr int W = VS + H - 1;
+    T av[W], dv[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) av[k] = a[k];
+    if (drow) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const int u = u0 + k;
+        dv[k] = (u >= 0 && u < nc) ? T(Storage<S>::load(drow, u)) : T(0);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < W; ++k) dv[k] = T(0);
+    }
+#pragma unroll
+    for (int q = 0; q < VS; ++q) {
+      T so = T(0), se = T(0);
+#pragma unroll
+      for (int t = 0; t < H; ++t) {
+        se = fma(h0[2 * t], av[q + t], se);
+        se = fma(h1[2 * t], dv[q + t], se);
+        so = fma(h0[2 * t + 1], av[q + t], so);
+        so = fma(h1[2 * t + 1], dv[q + t], so);
+      }
+      zo[q] = so;
+      ze[q] = se;
+    }
+  } else {
+    const int H = L / 2;
+#pragma unroll
+    for (int q = 0; q < VS; ++q) {
+      T so = T(0), se = T(0);
+      for (int t = 0; t < H; ++t) {
+        const T av = a[q + t];
+        const int u = u0 + q + t;
+        const T dv = (drow && u >= 0 && u < nc) ? T(Storage<S>::load(drow, u)) : T(0);
+        se = fma(h0[2 * t], av, se);
+        se = fma(h1[2 * t], dv, se);
+        so = fma(h0[2 * t + 1], av, so);
+        so = fma(h1[2 * t + 1], dv, so);
+      }
+      zo[q] = so;
+      ze[q] = se;
+    }
+  }
+}
+
+// Value of z at one extended position p (used for the few positions outside [0, n) that are
+// folded back).  The low band comes from LDS (a_lds[u], zero margins) or, when a_lds is
+// null, from the global row a_glob (null = zeros); d from the global row drow (null = zeros).
+template <typename S, typename T>
+__device__ inline T synthesis_point(const T* __restrict__ a_lds, const S* __restrict__ a_glob,
+                                    const S* __restrict__ drow, int p, int off, int nc,
+                                    const T* h0, const T* h1, int L) {
+  const int r = p - off;
+  const int par = r & 1;            // odd r: taps 2t + 1
+  const int u = (r + par) >> 1;     // floor division for negative r as well
+  T z = T(0);
+  for (int t = 0; t < L / 2; ++t) {
+    const int o = u + t;
+    if (o < 0 || o >= nc) continue;
+    const T av = a_lds ? a_lds[o] : (a_glob ? T(Storage<S>::load(a_glob, o)) : T(0));
+    z = fma(h0[2 * t + par], av, z);
+    if (drow) z = fma(h1[2 * t + par], T(Storage<S>::load(drow, o)), z);
+  }
+  return z;
+}
+
+// Fill the extension margins of an LDS signal buf (index = p - pmin) of length n for
+// positions p in [pmin, -1] and [n, pmax].
+template <typename T>
+__device__ inline void fill_margins(T* buf, int n, int pmin, int pmax, int mode) {
+  const int P = mode_period(mode, n);
+  const int left = -pmin;                      // positions pmin .. -1
+  const int right = pmax >= n ? pmax - n + 1 : 0;
+  for (int k = threadIdx.x; k < left + right; k += NT) {
+    const int p = k < left ? pmin + k : n + (k - left);
+    bool valid;
+    const int i = ext_index(p, n, mode, P, valid);
+    buf[p - pmin] = valid ? buf[i - pmin] : T(0);
+  }
+}
+
+template <typename T>
+__device__ inline void load_taps(const T* __restrict__ g0, const T* __restrict__ g1, T* s0,
+                                 T* s1, int L, bool reverse) {
+  for (int k = threadIdx.x; k < L; k += NT) {
+    const int j = reverse ? L - 1 - k : k;
+    s0[k] = g0[j];
+    s1[k] = g1[j];
+  }
+}
+
+// ------------------------------------------------------------------ analysis chain
+// One workgroup per row (grid = rows), or, in split mode (levels == 1), `split` chunks of
+// CO outputs per workgroup (grid = rows * workgroups_per_row).
+template <typename S, typename T, int LT>
+__global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int64_t rows,
+                                                            int wg_per_row) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* const A = reinterpret_cast<T*>(smem_raw);
+  T* const B = A + args.capA;
+  T* const tap_lds = B + args.capB;  // runtime-length taps (LT == 0)
+
+  const int64_t row = blockIdx.x / wg_per_row;
+  const int part = blockIdx.x % wg_per_row;
+  const int L = LT > 0 ? LT : args.taps;
+  const int off = args.off;
+  const int pmin = off - (L - 1);
+  const int mode = args.mode;
+  const int tid = threadIdx.x;
+
+  const T* gh0 = static_cast<const T*>(args.h0);
+  const T* gh1 = static_cast<const T*>(args.h1);
+  T hr0r[LT > 0 ? LT : 1], hr1r[LT > 0 ? LT : 1];
+  const T* hr0;
+  const T* hr1;
+  if constexpr (LT > 0) {
+#pragma unroll
+    for (int i = 0; i < LT; ++i) {
+      hr0r[i] = gh0[LT - 1 - i];
+      hr1r[i] = gh1[LT - 1 - i];
+    }
+    hr0 = hr0r;
+    hr1 = hr1r;
+  } else {
+    load_taps(gh0, gh1, tap_lds, tap_lds + L, L, true);
+    hr0 = tap_lds;
+    hr1 = tap_lds + L;
+    __syncthreads();
+  }
+
+  // ---- level 0: stream x through the staging window B in chunks of CO outputs
+  {
+    const int n = args.n_in[0];
+    const int no = args.n_out[0];
+    const int mode0 = normalize_mode(mode, n);
+    const int P = mode_period(mode0, n);
+    const S* xrow = static_cast<const S*>(args.x) + row * (int64_t)n;
+    S* drow = static_cast<S*>(args.details[0]) + row * (int64_t)no;
+    const bool last = args.levels == 1;
+    S* arow = last ? static_cast<S*>(args.approx) + row * (int64_t)no : nullptr;
+
+    const int nchunks = (int)cdiv(no, CO);
+    int c_begin = 0, c_end = nchunks;
+    if (args.split) {
+      c_begin = part * args.split;
+      c_end = min(nchunks, c_begin + args.split);
+    }
+    constexpr int SPAN_MAX = 2 * CO + (LT > 0 ? LT : MAXL_T) - 2;
+    constexpr int PF = (SPAN_MAX + NT - 1) / NT;  // prefetch registers (template length)
+    T pf[PF];
+
+    auto fetch = [&](int c, T (&r)[PF]) {
+      const int p0 = 2 * c * CO + pmin;
+      const bool interior = p0 >= 0 && p0 + SPAN_MAX <= n;
+#pragma unroll
+      for (int k = 0; k < PF; ++k) {
+        const int idx = tid + k * NT;
+        const int p = p0 + idx;
+        T v = T(0);
+        if (idx < SPAN_MAX) {
+          if (interior) {
+            v = T(Storage<S>::load(xrow, p));
+          } else {
+            bool valid = true;
+            int i = p;
+            if (p < 0 || p >= n) i = ext_index(p, n, mode0, P, valid);
+            if (valid) v = T(Storage<S>::load(xrow, i));
+          }
+        }
+        r[k] = v;
+      }
+    };
+
+    if (LT > 0 || L <= MAXL_T) {
+      if (c_begin < c_end) fetch(c_begin, pf);
+      for (int c = c_begin; c < c_end; ++c) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+          const int idx = tid + k * NT;
+          if (idx < SPAN_MAX) B[idx] = pf[k];
+        }
+        __syncthreads();
+        if (c + 1 < c_end) fetch(c + 1, pf);
+#pragma unroll
+        for (int g = 0; g < GA; ++g) {
+          const int lo = (g * NT + tid) * VA;  // output offset inside the chunk
+          const int o = c * CO + lo;
+          if (o >= no) break;
+          T y0[VA], y1[VA];
+          analysis_pair<T, LT>(B + 2 * lo, hr0, hr1, L, y0, y1);
+#pragma unroll
+          for (int q = 0; q < VA; ++q) {
+            if (o + q < no) {
+              Storage<S>::store(drow, o + q, y1[q]);
+              if (last) Storage<S>::store(arow, o + q, y0[q]);
+              else A[o + q - pmin] = y0[q];
+            }
+          }
+        }
+      }
+    } else {
+      // long runtime filters: stage without register prefetch (span depends on L)
+      const int span_max = 2 * CO + L - 2;
+      for (int c = c_begin; c < c_end; ++c) {
+        const int p0 = 2 * c * CO + pmin;
+        __syncthreads();
+        for (int idx = tid; idx < span_max; idx += NT) {
+          const int p = p0 + idx;
+          bool valid = true;
+          const int i = (p >= 0 && p < n) ? p : ext_index(p, n, mode0, P, valid);
+          B[idx] = valid ? T(Storage<S>::load(xrow, i)) : T(0);
+        }
+        __syncthreads();
+        for (int g = 0; g < GA; ++g) {
+          const int lo = (g * NT + tid) * VA;
+          const int o = c * CO + lo;
+          if (o >= no) break;
+          T y0[VA], y1[VA];
+          analysis_pair<T, 0>(B + 2 * lo, hr0, hr1, L, y0, y1);
+          for (int q = 0; q < VA; ++q) {
+            if (o + q < no) {
+              Storage<S>::store(drow, o + q, y1[q]);
+              if (last) Storage<S>::store(arow, o + q, y0[q]);
+              else A[o + q - pmin] = y0[q];
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // ---- levels 1 .. levels-1: the low band stays in LDS (A -> B -> A ...)
+  T* src = A;
+  T* dst = B;
+  for (int l = 1; l < args.levels; ++l) {
+    const int n = args.n_in[l];
+    const int no = args.n_out[l];
+    const int prev = args.n_out[l - 1];
+    // zero tail (waverec trim transpose), then the extension margins
+    if (tid == 0 && n > prev) src[prev - pmin] = T(0);
+    __syncthreads();
+    fill_margins(src, n, pmin, 2 * (no - 1) + off, normalize_mode(mode, n));
+    __syncthreads();
+    const bool last = l + 1 == args.levels;
+    S* drow = static_cast<S*>(args.details[l]) + row * (int64_t)no;
+    S* arow = last ? static_cast<S*>(args.approx) + row * (int64_t)no : nullptr;
+    for (int lo = tid * VA; lo < no; lo += NT * VA) {
+      T y0[VA], y1[VA];
+      analysis_pair<T, LT>(src + 2 * lo, hr0, hr1, L, y0, y1);
+#pragma unroll
+      for (int q = 0; q < VA; ++q) {
+        if (lo + q < no) {
+          Storage<S>::store(drow, lo + q, y1[q]);
+          if (last) Storage<S>::store(arow, lo + q, y0[q]);
+          else dst[lo + q - pmin] = y0[q];
+        }
+      }
+    }
+    T* t = src;
+    src = dst;
+    dst = t;
+  }
+}
+
+// ------------------------------------------------------------------ synthesis chain
+// Low band buffers are indexed buf[u + ZL] with zeros for u < 0 and u >= nc.
+template <typename S, typename T, int LT>
+__global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, int64_t rows,
+                                                             int wg_per_row) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* const A = reinterpret_cast<T*>(smem_raw);
+  T* const B = A + args.capA;
+  T* const E = B + args.capB;
+  T* const tap_lds = E + args.capE;
+
+  const int64_t row = blockIdx.x / wg_per_row;
+  const int part = blockIdx.x % wg_per_row;
+  const int L = LT > 0 ? LT : args.taps;
+  const int ZL = L;                      // left zero margin of low-band buffers
+  const int off = args.off;
+  const int mode = args.mode;
+  const int tid = threadIdx.x;
+
+  const T* gh0 = static_cast<const T*>(args.h0);
+  const T* gh1 = static_cast<const T*>(args.h1);
+  T h0r[LT > 0 ? LT : 1], h1r[LT > 0 ? LT : 1];
+  const T* h0;
+  const T* h1;
+  if constexpr (LT > 0) {
+#pragma unroll
+    for (int i = 0; i < LT; ++i) {
+      h0r[i] = gh0[i];
+      h1r[i] = gh1[i];
+    }
+    h0 = h0r;
+    h1 = h1r;
+  } else {
+    load_taps(gh0, gh1, tap_lds, tap_lds + L, L, false);
+    h0 = tap_lds;
+    h1 = tap_lds + L;
+  }
+
+  // stage the coarsest low band (or, in split mode, this workgroup's window of it)
+  int u_lo = 0;  // first staged coefficient index (split mode only)
+  {
+    const int nc = args.nc[0];
+    const S* ag = args.approx ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
+    if (args.split) {
+      // positions [i0, i1) need u in [(i0 - off) / 2 - 1, (i1 - off) / 2 + L / 2 + VS]
+      const int i0 = part * args.split;
+      u_lo = ((i0 - off) >> 1) - 2;
+    }
+    for (int k = tid; k < args.capA; k += NT) {
+      const int u = u_lo + k - ZL;
+      A[k] = (ag && u >= 0 && u < nc) ? T(Storage<S>::load(ag, u)) : T(0);
+    }
+  }
+  __syncthreads();
+
+  T* src = A;
+  T* dst = B;
+  for (int l = 0; l < args.levels; ++l) {
+    const int nc = args.nc[l];
+    const int m = args.n_out[l];
+    const bool last = l + 1 == args.levels;
+    const S* drow = args.details[l] ? static_cast<const S*>(args.details[l]) + row * (int64_t)nc
+                                    : nullptr;
+    const T* a0 = src + ZL - u_lo;  // a0[u] = low band coefficient u
+    const int md = normalize_mode(mode, m);
+    const int P = mode_period(md, m);
+
+    // positions outside [0, m) whose value folds back onto the row
+    const int pmin = off - (L - 1);
+    const int pmax = 2 * (nc - 1) + off;
+    const int nleft = md == FDWT_MODE_ZERO ? 0 : max(0, -pmin);
+    const int nright = md == FDWT_MODE_ZERO ? 0 : max(0, pmax - m + 1);
+    const int nextra = nleft + nright;
+    const S* ag = (args.split && args.approx)
+                      ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
+    for (int k = tid; k < nextra; k += NT) {
+      const int p = k < nleft ? pmin + k : m + (k - nleft);
+      E[k] = synthesis_point<S, T>(args.split ? nullptr : a0, ag, drow, p, off, nc, h0, h1, L);
+    }
+    __syncthreads();
+
+    int i_begin = 0, i_end = m;
+    if (args.split) {
+      i_begin = part * args.split;
+      i_end = min(m, i_begin + args.split);
+    }
+    // positions closer than this to an end may receive extras (reflect lands one further)
+    const int band = nextra + 2;
+    const int us = (i_begin + 1 - off) >> 1;  // first u whose pair touches i_begin
+    S* orow = last ? static_cast<S*>(args.out) + row * (int64_t)m : nullptr;
+    for (int ub = us + tid * VS; 2 * ub + off - 1 < i_end; ub += NT * VS) {
+      T zo[VS], ze[VS];
+      synthesis_pair<S, T, LT>(a0 + ub, drow, ub, nc, h0, h1, L, zo, ze);
+#pragma unroll
+      for (int q = 0; q < VS; ++q) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int i = 2 * (ub + q) + off - 1 + e;
+          if (i < i_begin || i >= i_end) continue;
+          T v = e ? ze[q] : zo[q];
+          if (i < band || i >= m - band) {
+            for (int k = 0; k < nextra; ++k) {
+              const int p = k < nleft ? pmin + k : m + (k - nleft);
+              bool valid;
+              if (ext_index(p, m, md, P, valid) == i && valid) v += E[k];
+            }
+          }
+          if (last) Storage<S>::store(orow, i, v);
+          else dst[ZL + i] = v;
+        }
+      }
+    }
+    __syncthreads();
+    if (!last) {
+      // zero margins of the next low band (which is the first nc[l+1] outputs)
+      const int ncn = args.nc[l + 1];
+      const int cap_dst = (l % 2 == 0) ? args.capB : args.capA;  // dst is B after even levels
+      for (int k = tid; k < ZL; k += NT) dst[k] = T(0);
+      for (int k = ZL + ncn + tid; k < cap_dst; k += NT) dst[k] = T(0);
+      __syncthreads();
+      T* t = src;
+      src = dst;
+      dst = t;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host side
+template <typename S>
+struct Dispatch;
+
+inline bool fits_lds(int64_t bytes) { return bytes <= 160 * 1024; }
+
+template <typename K>
+inline void set_lds(K kernel, size_t bytes) {
+  if (bytes > 64 * 1024)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+template <typename S, typename T, int LT>
+int launch_achain(const AChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
+                  hipStream_t st) {
+  auto k = analysis_chain_kernel<S, T, LT>;
+  set_lds(k, lds);
+  hipLaunchKernelGGL(k, dim3((unsigned)(rows * wg_per_row)), dim3(NT), lds, st, a, rows,
+                     wg_per_row);
+  FDWT_CHECK_LAUNCH();
+  return 0;
+}
+
+template <typename S, typename T, int LT>
+int launch_schain(const SChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
+                  hipStream_t st) {
+  auto k = synthesis_chain_kernel<S, T, LT>;
+  set_lds(k, lds);
+  hipLaunchKernelGGL(k, dim3((unsigned)(rows * wg_per_row)), dim3(NT), lds, st, a, rows,
+                     wg_per_row);
+  FDWT_CHECK_LAUNCH();
+  return 0;
+}
+
+#define FDWT_TAPS_SWITCH(L, FN, ...)                                                     \
+  switch (L) {                                                                           \
+    case 2: return FN<S, float, 2>(__VA_ARGS__);                                         \
+    case 4: return FN<S, float, 4>(__VA_ARGS__);                                         \
+    case 6: return FN<S, float, 6>(__VA_ARGS__);                                         \
+    case 8: return FN<S, float, 8>(__VA_ARGS__);                                         \
+    case 10: return FN<S, float, 10>(__VA_ARGS__);                                       \
+    case 12: return FN<S, float, 12>(__VA_ARGS__);                                       \
+    case 14: return FN<S, float, 14>(__VA_ARGS__);                                       \
+    case 16: return FN<S, float, 16>(__VA_ARGS__);                                       \
+    case 18: return FN<S, float, 18>(__VA_ARGS__);                                       \
+    case 20: return FN<S, float, 20>(__VA_ARGS__);                                       \
+    case 22: return FN<S, float, 22>(__VA_ARGS__);                                       \
+    case 24: return FN<S, float, 24>(__VA_ARGS__);                                       \
+    case 26: return FN<S, float, 26>(__VA_ARGS__);                                       \
+    case 28: return FN<S, float, 28>(__VA_ARGS__);                                       \
+    case 30: return FN<S, float, 30>(__VA_ARGS__);                                       \
+    case 32: return FN<S, float, 32>(__VA_ARGS__);                                       \
+    default: return FN<S, float, 0>(__VA_ARGS__);                                        \
+  }
+
+template <typename S>
+int run_achain(const AChainArgs& a, int64_t rows, int wg, size_t lds, hipStream_t st,
+               bool templated) {
+  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_achain, a, rows, wg, lds, st) }
+  return launch_achain<S, float, 0>(a, rows, wg, lds, st);
+}
+
+template <typename S>
+int run_schain(const SChainArgs& a, int64_t rows, int wg, size_t lds, hipStream_t st,
+               bool templated) {
+  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_schain, a, rows, wg, lds, st) }
+  return launch_schain<S, float, 0>(a, rows, wg, lds, st);
+}
+
+int dispatch_achain(const AChainArgs& a, int64_t rows, int wg, size_t lds, int dtype,
+                    hipStream_t st) {
+  const bool templ = a.taps <= MAXL_T;
+  switch (dtype) {
+    case FDWT_F32: return run_achain<float>(a, rows, wg, lds, st, templ);
+    case FDWT_F16: return run_achain<__half>(a, rows, wg, lds, st, templ);
+    case FDWT_BF16: return run_achain<bf16_t>(a, rows, wg, lds, st, templ);
+    case FDWT_F64: return launch_achain<double, double, 0>(a, rows, wg, lds, st);
+    default: return FDWT_ERR_ARG;
+  }
+}
+
+int dispatch_schain(const SChainArgs& a, int64_t rows, int wg, size_t lds, int dtype,
+                    hipStream_t st) {
+  const bool templ = a.taps <= MAXL_T;
+  switch (dtype) {
+    case FDWT_F32: return run_schain<float>(a, rows, wg, lds, st, templ);
+    case FDWT_F16: return run_schain<__half>(a, rows, wg, lds, st, templ);
+    case FDWT_BF16: return run_schain<bf16_t>(a, rows, wg, lds, st, templ);
+    case FDWT_F64: return launch_schain<double, double, 0>(a, rows, wg, lds, st);
+    default: return FDWT_ERR_ARG;
+  }
+}
+
+inline int compute_size(int dtype) { return dtype == FDWT_F64 ? 8 : 4; }
+
+inline bool valid_common(int64_t rows, int taps, int mode, int dtype) {
+  return rows >= 0 && taps >= 2 && taps % 2 == 0 && taps <= 4096 && mode >= 0 && mode <= 4 &&
+         dtype >= 0 && dtype <= 3;
+}
+
+// LDS layout of an analysis chain: A holds the inputs of odd levels, B the staging window of
+// level 0 and the inputs of even levels >= 2; sizes in compute elements.
+void achain_caps(const int64_t* n_in, const int64_t* n_out, int levels, int L, int* capA,
+                 int* capB) {
+  const int64_t stage = 2 * (int64_t)CO + (L > MAXL_T ? L : MAXL_T) - 2;
+  int64_t a = 0, b = stage;
+  for (int l = 1; l < levels; ++l) {
+    const int64_t need = std::max<int64_t>(2 * n_out[l] + L, n_in[l] + L) + 2;
+    if (l % 2) a = std::max(a, need);
+    else b = std::max(b, need);
+  }
+  *capA = (int)((a + 3) & ~3);
+  *capB = (int)((b + 3) & ~3);
+}
+
+int extras_count(int64_t nc, int64_t m, int L, int off, int mode) {
+  if (normalize_mode(mode, (int)m) == FDWT_MODE_ZERO) return 0;
+  const int64_t pmin = off - (L - 1);
+  const int64_t pmax = 2 * (nc - 1) + off;
+  return (int)(std::max<int64_t>(0, -pmin) + std::max<int64_t>(0, pmax - m + 1));
+}
+
+void schain_caps(const int64_t* nc, const int64_t* n_out, int levels, int L, int off, int mode,
+                 int split, int* capA, int* capB, int* capE) {
+  const int64_t margin = 2 * (int64_t)L + 2 * VS + 8;
+  int64_t a, b = 0, e = 4;
+  if (split) a = split / 2 + margin + 8;
+  else a = nc[0] + margin;
+  for (int l = 0; l < levels; ++l) {
+    e = std::max<int64_t>(e, extras_count(nc[l], n_out[l], L, off, mode));
+    if (l + 1 == levels) break;
+    const int64_t need = n_out[l] + margin;  // output of level l = low band of level l + 1
+    if (l % 2 == 0) b = std::max(b, need);
+    else a = std::max(a, need);
+  }
+  *capA = (int)((a + 3) & ~3);
+  *capB = (int)((b + 3) & ~3);
+  *capE = (int)((e + 3) & ~3);
+}
+
+}  // namespace
+}  // namespace fdwt
+
+using namespace fdwt;
+
+extern "C" int64_t fdwt_chain_max_length(int32_t taps, int32_t dtype) {
+  // analysis: A ~ n/2 + 2L, B ~ max(stage, n/4 + 2L); synthesis: similar.  Keep <= 160 KiB.
+  const int64_t budget = 160 * 1024 / compute_size(dtype) - 4 * (int64_t)taps - 4 * MAXL_T - 64;
+  const int64_t stage = 2 * (int64_t)CO + MAXL_T;
+  // n/2 + max(stage, n/4) + 6L <= budget
+  int64_t n = 2 * (budget - stage - 6 * (int64_t)taps);
+  const int64_t n2 = (budget - 6 * (int64_t)taps) * 4 / 3;
+  if (n2 / 4 > stage) n = n2;  // the n/4 term dominates the staging window
+  return n > 0 ? n : 0;
+}
+
+extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* approx,
+                                   const void* h0, const void* h1, int64_t rows,
+                                   const int64_t* n_in, const int64_t* n_out, int32_t levels,
+                                   int32_t taps, int32_t mode, int32_t off, int32_t dtype,
+                                   void* stream) {
+  if (!valid_common(rows, taps, mode, dtype) || levels < 1 || levels > FDWT_MAX_LEVELS ||
+      !n_in || !n_out)
+    return FDWT_ERR_ARG;
+  if (rows == 0) return 0;
+  AChainArgs a{};
+  for (int l = 0; l < levels; ++l) {
+    if (n_in[l] < 1 || n_out[l] < 1 || n_in[l] > INT32_MAX / 2 || n_out[l] > INT32_MAX / 4)
+      return FDWT_ERR_ARG;
+    if (l > 0 && (n_in[l] < n_out[l - 1] || n_in[l] > n_out[l - 1] + 1)) return FDWT_ERR_ARG;
+    if (!details || !details[l]) return FDWT_ERR_ARG;
+    a.details[l] = details[l];
+    a.n_in[l] = (int32_t)n_in[l];
+    a.n_out[l] = (int32_t)n_out[l];
+  }
+  if (!x || !approx || !h0 || !h1) return FDWT_ERR_ARG;
+  // the extension must stay within one row period of the signal's support: guaranteed by
+  // n_out <= (n + L - 1) / 2 + 1 for every mode
+  for (int l = 0; l < levels; ++l)
+    if (2 * (n_out[l] - 1) + off > n_in[l] + 2 * (int64_t)taps + 2) return FDWT_ERR_ARG;
+  a.x = x;
+  a.approx = approx;
+  a.h0 = h0;
+  a.h1 = h1;
+  a.levels = levels;
+  a.taps = taps;
+  a.mode = mode;  // normalised per level in the kernel (reflect on one sample)
+  a.off = off;
+  if (off < 0 || off > taps) return FDWT_ERR_ARG;
+  int capA, capB;
+  achain_caps(n_in, n_out, levels, taps, &capA, &capB);
+  a.capA = capA;
+  a.capB = capB;
+  const int cs = compute_size(dtype);
+  const size_t lds = (size_t)(capA + capB + 2 * taps + 4) * cs;
+  if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
+  int wg = 1;
+  a.split = 0;
+  const int64_t nchunks = cdiv(n_out[0], CO);
+  if (levels == 1 && rows < 1024 && nchunks > 1) {
+    // few long rows: spread the chunks of a row over several workgroups
+    const int64_t want = cdiv(2048, rows);
+    a.split = (int)std::max<int64_t>(1, cdiv(nchunks, want));
+    wg = (int)cdiv(nchunks, a.split);
+  }
+  if (rows * wg > INT32_MAX) return FDWT_ERR_ARG;
+  return dispatch_achain(a, rows, wg, lds, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* details, void* out,
+                                    const void* h0, const void* h1, int64_t rows,
+                                    const int64_t* nc, const int64_t* n_out, int32_t levels,
+                                    int32_t taps, int32_t mode, int32_t off, int32_t dtype,
+                                    void* stream) {
+  if (!valid_common(rows, taps, mode, dtype) || levels < 1 || levels > FDWT_MAX_LEVELS ||
+      !nc || !n_out || !out || !h0 || !h1)
+    return FDWT_ERR_ARG;
+  if (rows == 0) return 0;
+  SChainArgs a{};
+  for (int l = 0; l < levels; ++l) {
+    if (nc[l] < 1 || n_out[l] < 1 || nc[l] > INT32_MAX / 4 || n_out[l] > INT32_MAX / 2)
+      return FDWT_ERR_ARG;
+    if (l > 0 && (nc[l] > n_out[l - 1] || nc[l] < n_out[l - 1] - 1)) return FDWT_ERR_ARG;
+    // every output position must be reachable by the coefficients' taps
+    if (n_out[l] > 2 * nc[l] + 2) return FDWT_ERR_ARG;
+    a.details[l] = details ? details[l] : nullptr;
+    a.nc[l] = (int32_t)nc[l];
+    a.n_out[l] = (int32_t)n_out[l];
+  }
+  if (off < 0 || off > taps) return FDWT_ERR_ARG;
+  a.approx = approx;
+  a.out = out;
+  a.h0 = h0;
+  a.h1 = h1;
+  a.levels = levels;
+  a.taps = taps;
+  a.mode = mode;
+  a.off = off;
+  int wg = 1;
+  a.split = 0;
+  const int64_t m = n_out[0];
+  if (levels == 1 && (rows < 1024 || nc[0] > fdwt_chain_max_length(taps, dtype) / 2) &&
+      m > 4096) {
+    const int64_t want = std::max<int64_t>(cdiv(2048, rows), cdiv(m, 16384));
+    int64_t per = std::max<int64_t>(1024, cdiv(m, want));
+    per = (per + 1023) & ~(int64_t)1023;
+    a.split = (int)per;
+    wg = (int)cdiv(m, per);
+  }
+  int capA, capB, capE;
+  schain_caps(nc, n_out, levels, taps, off, mode, a.split, &capA, &capB, &capE);
+  a.capA = capA;
+  a.capB = capB;
+  a.capE = capE;
+  const int cs = compute_size(dtype);
+  const size_t lds = (size_t)(capA + capB + capE + 2 * taps + 4) * cs;
+  if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
+  if (rows * wg > INT32_MAX) return FDWT_ERR_ARG;
+  return dispatch_schain(a, rows, wg, lds, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fdwt_dwt_analysis(const void* x, void* y0, void* y1, const void* h0,
+                                 const void* h1, int64_t rows, int64_t n, int64_t n_out,
+                                 int32_t taps, int32_t mode, int32_t off, int32_t dtype,
+                                 void* stream) {
+  void* det[1] = {y1};
+  return fdwt_analysis_chain(x, det, y0, h0, h1, rows, &n, &n_out, 1, taps, mode, off, dtype,
+                             stream);
+}
+
+extern "C" int fdwt_dwt_synthesis(const void* a, const void* d, void* y, const void* h0,
+                                  const void* h1, int64_t rows, int64_t nc, int64_t n,
+                                  int32_t taps, int32_t mode, int32_t off, int32_t dtype,
+                                  void* stream) {
+  const void* det[1] = {d};
+  return fdwt_synthesis_chain(a, det, y, h0, h1, rows, &nc, &n, 1, taps, mode, off, dtype,
+                              stream);
+}
