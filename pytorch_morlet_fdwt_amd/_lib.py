@@ -67,6 +67,52 @@ def lib():
     return _LIB
 
 
+class KernelTimer:
+    """Optional per-entry-point timing: when installed (``set_timer``), every launch made
+    through :func:`launch` is bracketed by HIP events on the stream it is enqueued on.
+    ``summary()`` then gives, per entry point, the number of launches and their mean
+    duration (ms), read after a synchronize."""
+
+    def __init__(self):
+        self.events = {}
+
+    def record(self, name, device):
+        s = torch.cuda.current_stream(device)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        return e0, e1, s
+
+    def summary(self):
+        out = {}
+        for name, evs in self.events.items():
+            ts = [a.elapsed_time(b) for a, b in evs]
+            out[name] = (len(ts), sum(ts) / max(1, len(ts)))
+        return out
+
+
+_TIMER = None
+
+
+def set_timer(timer):
+    global _TIMER
+    _TIMER = timer
+
+
+def launch(name: str, device, *args):
+    """Call entry point ``name`` with ``args`` on ``device`` and raise on failure."""
+    fn = getattr(lib(), name)
+    with torch.cuda.device(device):
+        if _TIMER is None:
+            check(fn(*args), name)
+            return
+        e0, e1, s = _TIMER.record(name, device)
+        code = fn(*args)
+        e1.record(s)
+        _TIMER.events.setdefault(name, []).append((e0, e1))
+        check(code, name)
+
+
 def check(code: int, what: str = ""):
     if code != 0:
         msg = lib().fdwt_error_string(code).decode()

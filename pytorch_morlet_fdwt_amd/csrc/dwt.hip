@@ -16,18 +16,23 @@
 //    prefetched into registers while the current chunk is computed.
 //  * Split kernels (one level, several workgroups per row) serve rows too long for LDS.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
 namespace fdwt {
 namespace {
 
-constexpr int NT = 256;          // threads per workgroup (4 wave64)
+constexpr int NT = 512;          // threads per workgroup (8 wave64): two resident rows per
+                                 // CU then keep enough loads in flight to cover HBM latency
 constexpr int VA = 2;            // consecutive analysis outputs per thread
-constexpr int GA = 4;            // thread groups per analysis chunk
+constexpr int GA = 2;            // thread groups per analysis chunk
 constexpr int CO = NT * VA * GA; // outputs per analysis chunk (2048)
 constexpr int VS = 2;            // consecutive synthesis pairs (u values) per thread
+constexpr int GS = 4;            // thread groups per synthesis pass
+constexpr int PS = NT * VS * GS; // coefficient pairs per synthesis pass (4096)
 constexpr int MAXL_T = 32;       // largest templated filter length
+constexpr int MAX_TAPS = 256;    // longest filter accepted (PyWavelets' longest is 102)
 
 struct AChainArgs {
   const void* x;
@@ -51,19 +56,37 @@ struct SChainArgs {
   int32_t nc[FDWT_MAX_LEVELS];
   int32_t n_out[FDWT_MAX_LEVELS];
   int32_t levels, taps, mode, off;
-  int32_t capA, capB, capE;
+  int32_t capA, capB, capE, capD;
   int32_t split;  // output positions per workgroup in split mode (levels == 1), 0 = row
 };
 
 // ------------------------------------------------------------------ compute windows
+// Read W consecutive LDS elements starting at an address aligned to V elements with V-wide
+// vector loads (ds_read_b64 / ds_read_b128); neighbouring lanes then read neighbouring
+// words, which keeps the access free of bank conflicts.  May read up to V - 1 elements past
+// the window.
+template <int V, typename T, int W>
+__device__ inline void lds_window(const T* __restrict__ p, T (&w)[W]) {
+  typedef T vec __attribute__((ext_vector_type(V)));
+  const vec* q = reinterpret_cast<const vec*>(p);
+#pragma unroll
+  for (int v = 0; v < (W + V - 1) / V; ++v) {
+    const vec t = q[v];
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      if (V * v + e < W) w[V * v + e] = t[e];
+  }
+}
+
+// VA consecutive analysis outputs of both bands from the extended window s (16-byte
+// aligned): y_b[q] = sum_i hr_b[i] s[2 q + i] with hr_b the reversed filter.
 template <typename T, int LT>
 __device__ inline void analysis_pair(const T* __restrict__ s, const T* hr0, const T* hr1,
                                      int L, T (&y0)[VA], T (&y1)[VA]) {
   if constexpr (LT > 0) {
     constexpr int W = 2 * VA + LT - 2;
     T w[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) w[k] = s[k];
+    lds_window<(sizeof(T) == 4 ? 4 : 2)>(s, w);  // windows start 2 * VA = 4 elements apart
 #pragma unroll
     for (int q = 0; q < VA; ++q) {
       T a0 = T(0), a1 = T(0);
@@ -91,27 +114,18 @@ __device__ inline void analysis_pair(const T* __restrict__ s, const T* hr0, cons
 }
 
 // z_odd[q] (position off + 2(u0+q) - 1) and z_even[q] (position off + 2(u0+q)) from the
-// low band a[u0 ..] (LDS, zero margins) and the high band d[u0 ..] (global, bounds checked).
-template <typename S, typename T, int LT>
-__device__ inline void synthesis_pair(const T* __restrict__ a, const S* __restrict__ drow,
-                                      int u0, int nc, const T* h0, const T* h1, int L,
-                                      T (&zo)[VS], T (&ze)[VS]) {
+// low band a[0..] and the high band d[0..], both LDS windows starting at coefficient u0
+// (16-byte aligned, zero outside the coefficients).
+template <typename T, int LT>
+__device__ inline void synthesis_block(const T* __restrict__ a, const T* __restrict__ d,
+                                       const T* h0, const T* h1, int L, T (&zo)[VS],
+                                       T (&ze)[VS]) {
   if constexpr (LT > 0) {
     constexpr int H = LT / 2;
     constexpr int W = VS + H - 1;
     T av[W], dv[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) av[k] = a[k];
-    if (drow) {
-#pragma unroll
-      for (int k = 0; k < W; ++k) {
-        const int u = u0 + k;
-        dv[k] = (u >= 0 && u < nc) ? T(Storage<S>::load(drow, u)) : T(0);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < W; ++k) dv[k] = T(0);
-    }
+    lds_window<VS>(a, av);  // windows start VS elements apart (VS-aligned)
+    lds_window<VS>(d, dv);
 #pragma unroll
     for (int q = 0; q < VS; ++q) {
       T so = T(0), se = T(0);
@@ -132,8 +146,7 @@ __device__ inline void synthesis_pair(const T* __restrict__ a, const S* __restri
       T so = T(0), se = T(0);
       for (int t = 0; t < H; ++t) {
         const T av = a[q + t];
-        const int u = u0 + q + t;
-        const T dv = (drow && u >= 0 && u < nc) ? T(Storage<S>::load(drow, u)) : T(0);
+        const T dv = d[q + t];
         se = fma(h0[2 * t], av, se);
         se = fma(h1[2 * t], dv, se);
         so = fma(h0[2 * t + 1], av, so);
@@ -156,14 +169,50 @@ __device__ inline T synthesis_point(const T* __restrict__ a_lds, const S* __rest
   const int par = r & 1;            // odd r: taps 2t + 1
   const int u = (r + par) >> 1;     // floor division for negative r as well
   T z = T(0);
-  for (int t = 0; t < L / 2; ++t) {
-    const int o = u + t;
-    if (o < 0 || o >= nc) continue;
-    const T av = a_lds ? a_lds[o] : (a_glob ? T(Storage<S>::load(a_glob, o)) : T(0));
-    z = fma(h0[2 * t + par], av, z);
-    if (drow) z = fma(h1[2 * t + par], T(Storage<S>::load(drow, o)), z);
+  // taps in batches of 8 whose (clamped, unconditional) global loads are all in flight
+  // together; out-of-range coefficients are zeroed by select
+  for (int t0 = 0; t0 < L / 2; t0 += 8) {
+    T av[8], dv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int o = u + t0 + k;
+      const int oc = min(max(o, 0), nc - 1);
+      const bool ok = o >= 0 && o < nc && t0 + k < L / 2;
+      T a = a_lds ? a_lds[oc] : (a_glob ? T(Storage<S>::load(a_glob, oc)) : T(0));
+      T d = drow ? T(Storage<S>::load(drow, oc)) : T(0);
+      av[k] = ok ? a : T(0);
+      dv[k] = ok ? d : T(0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (t0 + k < L / 2) {
+        z = fma(h0[2 * (t0 + k) + par], av[k], z);
+        z = fma(h1[2 * (t0 + k) + par], dv[k], z);
+      }
+    }
   }
   return z;
+}
+
+// init + sum of the out-of-range values E[k] whose row position ET[k] is i, in k order.
+// The LDS reads are issued in batches of 8 so that they overlap.
+template <typename T>
+__device__ inline T fold_sum(const int* ET, const T* E, int nextra, int i, T init) {
+  T acc = init;
+  for (int k0 = 0; k0 < nextra; k0 += 8) {
+    int t[8];
+    T e[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int kk = min(k0 + k, nextra - 1);
+      t[k] = ET[kk];
+      e[k] = E[kk];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k0 + k < nextra && t[k] == i) acc += e[k];
+  }
+  return acc;
 }
 
 // Fill the extension margins of an LDS signal buf (index = p - pmin) of length n for
@@ -188,6 +237,51 @@ __device__ inline void load_taps(const T* __restrict__ g0, const T* __restrict__
     const int j = reverse ? L - 1 - k : k;
     s0[k] = g0[j];
     s1[k] = g1[j];
+  }
+}
+
+// Store VA consecutive outputs o.. of both bands: the high band to global memory, the low
+// band to global memory (arow, last level) or to LDS (lds[o]).  Paired stores when the
+// caller has established 8-byte alignment (o is even).
+template <typename S, typename T>
+__device__ inline void store_bands(S* drow, S* arow, T* lds, int o, int no, const T (&y0)[VA],
+                                   const T (&y1)[VA], bool vec_g, bool vec_l) {
+  static_assert(VA == 2, "paired stores assume two outputs per thread");
+  if (o + 1 < no) {
+    if constexpr (std::is_same<S, float>::value) {
+      if (vec_g) {
+        typedef float v2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<v2*>(drow + o) = v2{y1[0], y1[1]};
+        if (!lds) *reinterpret_cast<v2*>(arow + o) = v2{y0[0], y0[1]};
+      } else {
+        drow[o] = y1[0];
+        drow[o + 1] = y1[1];
+        if (!lds) {
+          arow[o] = y0[0];
+          arow[o + 1] = y0[1];
+        }
+      }
+    } else {
+      Storage<S>::store(drow, o, y1[0]);
+      Storage<S>::store(drow, o + 1, y1[1]);
+      if (!lds) {
+        Storage<S>::store(arow, o, y0[0]);
+        Storage<S>::store(arow, o + 1, y0[1]);
+      }
+    }
+    if (lds) {
+      if (vec_l) {
+        typedef T v2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<v2*>(lds + o) = v2{y0[0], y0[1]};
+      } else {
+        lds[o] = y0[0];
+        lds[o + 1] = y0[1];
+      }
+    }
+  } else if (o < no) {
+    Storage<S>::store(drow, o, y1[0]);
+    if (lds) lds[o] = y0[0];
+    else Storage<S>::store(arow, o, y0[0]);
   }
 }
 
@@ -241,6 +335,9 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
     const bool last = args.levels == 1;
     S* arow = last ? static_cast<S*>(args.approx) + row * (int64_t)no : nullptr;
 
+    // paired (8-byte) stores when rows stay 8-byte aligned: o is always even
+    const bool vec_g = std::is_same<S, float>::value && (no % 2) == 0;
+    const bool vec_l = (pmin & 1) == 0;
     const int nchunks = (int)cdiv(no, CO);
     int c_begin = 0, c_end = nchunks;
     if (args.split) {
@@ -263,10 +360,12 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
           if (interior) {
             v = T(Storage<S>::load(xrow, p));
           } else {
+            // unconditional load of a valid index, zeroed by select (zero padding)
             bool valid = true;
             int i = p;
             if (p < 0 || p >= n) i = ext_index(p, n, mode0, P, valid);
-            if (valid) v = T(Storage<S>::load(xrow, i));
+            const T w = T(Storage<S>::load(xrow, valid ? i : 0));
+            v = valid ? w : T(0);
           }
         }
         r[k] = v;
@@ -291,14 +390,8 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
           if (o >= no) break;
           T y0[VA], y1[VA];
           analysis_pair<T, LT>(B + 2 * lo, hr0, hr1, L, y0, y1);
-#pragma unroll
-          for (int q = 0; q < VA; ++q) {
-            if (o + q < no) {
-              Storage<S>::store(drow, o + q, y1[q]);
-              if (last) Storage<S>::store(arow, o + q, y0[q]);
-              else A[o + q - pmin] = y0[q];
-            }
-          }
+          store_bands<S, T>(drow, arow, last ? nullptr : A - pmin, o, no, y0, y1, vec_g,
+                            vec_l);
         }
       }
     } else {
@@ -347,17 +440,12 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
     const bool last = l + 1 == args.levels;
     S* drow = static_cast<S*>(args.details[l]) + row * (int64_t)no;
     S* arow = last ? static_cast<S*>(args.approx) + row * (int64_t)no : nullptr;
+    const bool vec_g = std::is_same<S, float>::value && (no % 2) == 0;
+    const bool vec_l = (pmin & 1) == 0;
     for (int lo = tid * VA; lo < no; lo += NT * VA) {
       T y0[VA], y1[VA];
       analysis_pair<T, LT>(src + 2 * lo, hr0, hr1, L, y0, y1);
-#pragma unroll
-      for (int q = 0; q < VA; ++q) {
-        if (lo + q < no) {
-          Storage<S>::store(drow, lo + q, y1[q]);
-          if (last) Storage<S>::store(arow, lo + q, y0[q]);
-          else dst[lo + q - pmin] = y0[q];
-        }
-      }
+      store_bands<S, T>(drow, arow, last ? nullptr : dst - pmin, lo, no, y0, y1, vec_g, vec_l);
     }
     T* t = src;
     src = dst;
@@ -366,7 +454,13 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
 }
 
 // ------------------------------------------------------------------ synthesis chain
-// Low band buffers are indexed buf[u + ZL] with zeros for u < 0 and u >= nc.
+// Low band buffers are indexed buf[u + ZL] (ZL = L rounded up to a multiple of 4) with zeros
+// for u < 0 and u >= nc.  Per level:
+//  1. the few extended positions outside [0, m) are evaluated (E) together with the row
+//     position they fold onto (ET), then reduced per edge position (F);
+//  2. the row is produced in passes of NT * VS coefficient pairs: the high band of a pass is
+//     staged in LDS (D) by coalesced loads, the next pass's prefetched into registers, and
+//     each thread computes 2 * VS consecutive positions from two aligned register windows.
 template <typename S, typename T, int LT>
 __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, int64_t rows,
                                                              int wg_per_row) {
@@ -374,12 +468,16 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
   T* const A = reinterpret_cast<T*>(smem_raw);
   T* const B = A + args.capA;
   T* const E = B + args.capB;
-  T* const tap_lds = E + args.capE;
+  int* const ET = reinterpret_cast<int*>(E + args.capE);
+  T* const F = reinterpret_cast<T*>(ET + args.capE);
+  T* const D = F + (2 * args.capE + 8);
+  T* const tap_lds = D + args.capD;
 
   const int64_t row = blockIdx.x / wg_per_row;
   const int part = blockIdx.x % wg_per_row;
   const int L = LT > 0 ? LT : args.taps;
-  const int ZL = L;                      // left zero margin of low-band buffers
+  const int H = L / 2;
+  const int ZL = (L + 3) & ~3;
   const int off = args.off;
   const int mode = args.mode;
   const int tid = threadIdx.x;
@@ -404,21 +502,52 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
   }
 
   // stage the coarsest low band (or, in split mode, this workgroup's window of it)
-  int u_lo = 0;  // first staged coefficient index (split mode only)
+  int u_lo = 0;
   {
     const int nc = args.nc[0];
     const S* ag = args.approx ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
-    if (args.split) {
-      // positions [i0, i1) need u in [(i0 - off) / 2 - 1, (i1 - off) / 2 + L / 2 + VS]
-      const int i0 = part * args.split;
-      u_lo = ((i0 - off) >> 1) - 2;
-    }
+    if (args.split) u_lo = ((((part * args.split) - off) >> 1) - 4) & ~3;
     for (int k = tid; k < args.capA; k += NT) {
       const int u = u_lo + k - ZL;
-      A[k] = (ag && u >= 0 && u < nc) ? T(Storage<S>::load(ag, u)) : T(0);
+      T v = T(0);
+      if (ag) {
+        const T w = T(Storage<S>::load(ag, min(max(u, 0), nc - 1)));
+        v = (u >= 0 && u < nc) ? w : T(0);
+      }
+      A[k] = v;
     }
   }
   __syncthreads();
+
+  // first coefficient pair of a level's passes (aligned to VS); whole-row workgroups of
+  // non-zero modes start at the extended range [pmin, ...) (see below)
+  auto level_first_pass = [&](int lv) {
+    const int ncl = args.nc[lv];
+    const int ml = args.n_out[lv];
+    const int mdl = normalize_mode(mode, ml);
+    const int pminl = off - (L - 1);
+    const int pmaxl = 2 * (ncl - 1) + off;
+    const int nx = mdl == FDWT_MODE_ZERO ? 0 : max(0, -pminl) + max(0, pmaxl - ml + 1);
+    const int ib = args.split ? part * args.split : 0;
+    const int pbeg = (nx > 0 && !args.split) ? min(0, pminl) : ib;
+    return ((pbeg + 1 - off) >> 1) & ~(VS - 1);
+  };
+  const int dspan = PS + H + 4;
+  constexpr int PFD = PS / NT + 1;  // dspan <= PFD * NT since H + 4 <= NT
+  T pf[PFD];
+  auto fetch_d = [&](const S* dr, int ncl, int pbl) {
+#pragma unroll
+    for (int k = 0; k < PFD; ++k) {
+      const int idx = tid + k * NT;
+      const int u = pbl + idx;
+      T v = T(0);
+      if (dr && idx < dspan) {
+        const T w = T(Storage<S>::load(dr, min(max(u, 0), ncl - 1)));
+        v = (u >= 0 && u < ncl) ? w : T(0);
+      }
+      pf[k] = v;
+    }
+  };
 
   T* src = A;
   T* dst = B;
@@ -432,49 +561,129 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
     const int md = normalize_mode(mode, m);
     const int P = mode_period(md, m);
 
-    // positions outside [0, m) whose value folds back onto the row
+    // 1. extended positions outside [0, m) fold back onto row positions near the ends (the
+    //    "band").  Whole-row workgroups run their passes over the extended range, park the
+    //    out-of-range values (E) and the band values (F) in LDS, and fold them after the
+    //    passes; split workgroups evaluate the out-of-range values up front instead.
     const int pmin = off - (L - 1);
     const int pmax = 2 * (nc - 1) + off;
     const int nleft = md == FDWT_MODE_ZERO ? 0 : max(0, -pmin);
     const int nright = md == FDWT_MODE_ZERO ? 0 : max(0, pmax - m + 1);
     const int nextra = nleft + nright;
+    const bool inpass = nextra > 0 && !args.split;
+    const int band = nextra ? nextra + 2 : 0;  // reflect folds one position further in
+    const bool small = m <= 2 * band;
+    const int nslot = nextra ? (small ? m : 2 * band) : 0;
     const S* ag = (args.split && args.approx)
                       ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
-    for (int k = tid; k < nextra; k += NT) {
-      const int p = k < nleft ? pmin + k : m + (k - nleft);
-      E[k] = synthesis_point<S, T>(args.split ? nullptr : a0, ag, drow, p, off, nc, h0, h1, L);
-    }
-    __syncthreads();
 
     int i_begin = 0, i_end = m;
     if (args.split) {
       i_begin = part * args.split;
       i_end = min(m, i_begin + args.split);
     }
-    // positions closer than this to an end may receive extras (reflect lands one further)
-    const int band = nextra + 2;
-    const int us = (i_begin + 1 - off) >> 1;  // first u whose pair touches i_begin
+    const int p_begin = inpass ? min(0, pmin) : i_begin;
+    const int p_end = inpass ? max(m, pmax + 1) : i_end;
+    const int ub0 = level_first_pass(l);
+    int pb = ub0;
+    if (l == 0 && 2 * pb + off - 1 < p_end) fetch_d(drow, nc, pb);  // later levels: prefetched
+
+    for (int k = tid; k < nextra; k += NT) {
+      const int p = k < nleft ? pmin + k : m + (k - nleft);
+      bool valid;
+      const int t = ext_index(p, m, md, P, valid);
+      ET[k] = valid ? t : -1;
+      if (!inpass)
+        E[k] = synthesis_point<S, T>(args.split ? nullptr : a0, ag, drow, p, off, nc, h0, h1, L);
+    }
+    if (!inpass && nextra) {
+      __syncthreads();
+      for (int sl = tid; sl < nslot; sl += NT) {
+        const int i = (small || sl < band) ? sl : m - 2 * band + sl;
+        F[sl] = fold_sum(ET, E, nextra, i, T(0));
+      }
+    }
+
+    // 2. the row, in passes of NT * VS * GS coefficient pairs
     S* orow = last ? static_cast<S*>(args.out) + row * (int64_t)m : nullptr;
-    for (int ub = us + tid * VS; 2 * ub + off - 1 < i_end; ub += NT * VS) {
-      T zo[VS], ze[VS];
-      synthesis_pair<S, T, LT>(a0 + ub, drow, ub, nc, h0, h1, L, zo, ze);
+    // 16-byte stores when provably aligned: off == 1 puts every thread's first position on
+    // a multiple of 4, and m % 4 == 0 keeps rows 16-byte aligned in global memory
+    const bool vec_out = std::is_same<S, float>::value && off == 1 && (m % 4) == 0;
+    const bool vec_lds = off == 1;
+    const int plain_lo = max(i_begin, band);
+    const int plain_hi = min(i_end, m - band);
+    for (; 2 * pb + off - 1 < p_end; pb += PS) {
+      __syncthreads();  // previous pass done with D (F / E / ET written)
 #pragma unroll
-      for (int q = 0; q < VS; ++q) {
+      for (int k = 0; k < PFD; ++k) {
+        const int idx = tid + k * NT;
+        if (idx < dspan) D[idx] = pf[k];
+      }
+      __syncthreads();
+      const int pn = pb + PS;
+      if (2 * pn + off - 1 < p_end) {
+        fetch_d(drow, nc, pn);
+      } else if (!last) {
+        // last pass of this level: request the first pass of the next level now
+        const int nl = l + 1;
+        fetch_d(args.details[nl] ? static_cast<const S*>(args.details[nl]) + row * (int64_t)args.nc[nl]
+                                 : nullptr,
+                args.nc[nl], level_first_pass(nl));
+      }
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int i = 2 * (ub + q) + off - 1 + e;
-          if (i < i_begin || i >= i_end) continue;
-          T v = e ? ze[q] : zo[q];
-          if (i < band || i >= m - band) {
-            for (int k = 0; k < nextra; ++k) {
-              const int p = k < nleft ? pmin + k : m + (k - nleft);
-              bool valid;
-              if (ext_index(p, m, md, P, valid) == i && valid) v += E[k];
-            }
-          }
-          if (last) Storage<S>::store(orow, i, v);
-          else dst[ZL + i] = v;
+      for (int g = 0; g < GS; ++g) {
+        const int lu = (g * NT + tid) * VS;  // coefficient offset inside the pass
+        const int ub = pb + lu;
+        const int i0 = 2 * ub + off - 1;     // first of this thread's 2 * VS positions
+        if (i0 >= p_end) continue;
+        T zo[VS], ze[VS];
+        synthesis_block<T, LT>(a0 + ub, D + lu, h0, h1, L, zo, ze);
+        T v[2 * VS];
+#pragma unroll
+        for (int q = 0; q < VS; ++q) {
+          v[2 * q] = zo[q];
+          v[2 * q + 1] = ze[q];
         }
+        if (VS == 2 && i0 >= plain_lo && i0 + 2 * VS <= plain_hi && (last ? vec_out : vec_lds)) {
+          typedef T v4 __attribute__((ext_vector_type(4)));
+          const v4 w = {v[0], v[1], v[2], v[3]};
+          if (last) {
+            if constexpr (std::is_same<S, float>::value)
+              *reinterpret_cast<v4*>(orow + i0) = w;
+          } else {
+            *reinterpret_cast<v4*>(dst + ZL + i0) = w;
+          }
+          continue;
+        }
+#pragma unroll
+        for (int j = 0; j < 2 * VS; ++j) {
+          const int i = i0 + j;
+          T val = v[j];
+          if (i >= i_begin && i < i_end) {
+            if (band && (i < band || i >= m - band)) {
+              const int sl = (small || i < band) ? i : i - (m - 2 * band);
+              if (inpass) {
+                F[sl] = val;  // folded once every out-of-range value exists
+                continue;
+              }
+              val += F[sl];
+            }
+            if (last) Storage<S>::store(orow, i, val);
+            else dst[ZL + i] = val;
+          } else if (inpass) {
+            if (i < 0 && i >= pmin) E[i - pmin] = val;
+            else if (i >= m && i <= pmax) E[nleft + i - m] = val;
+          }
+        }
+      }
+    }
+    if (inpass) {
+      __syncthreads();
+      for (int sl = tid; sl < nslot; sl += NT) {
+        const int i = (small || sl < band) ? sl : m - 2 * band + sl;
+        const T acc = fold_sum(ET, E, nextra, i, F[sl]);
+        if (last) Storage<S>::store(orow, i, acc);
+        else dst[ZL + i] = acc;
       }
     }
     __syncthreads();
@@ -498,18 +707,21 @@ struct Dispatch;
 
 inline bool fits_lds(int64_t bytes) { return bytes <= 160 * 1024; }
 
+// Raise the dynamic LDS limit of a kernel to the full 160 KiB.  Called once per kernel
+// instantiation through a function-local static of the (templated) launcher.
 template <typename K>
-inline void set_lds(K kernel, size_t bytes) {
-  if (bytes > 64 * 1024)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+inline bool allow_full_lds(K kernel) {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  return true;
 }
 
 template <typename S, typename T, int LT>
 int launch_achain(const AChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
                   hipStream_t st) {
   auto k = analysis_chain_kernel<S, T, LT>;
-  set_lds(k, lds);
+  static const bool lds_ok = allow_full_lds(k);
+  (void)lds_ok;
   hipLaunchKernelGGL(k, dim3((unsigned)(rows * wg_per_row)), dim3(NT), lds, st, a, rows,
                      wg_per_row);
   FDWT_CHECK_LAUNCH();
@@ -520,7 +732,8 @@ template <typename S, typename T, int LT>
 int launch_schain(const SChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
                   hipStream_t st) {
   auto k = synthesis_chain_kernel<S, T, LT>;
-  set_lds(k, lds);
+  static const bool lds_ok = allow_full_lds(k);
+  (void)lds_ok;
   hipLaunchKernelGGL(k, dim3((unsigned)(rows * wg_per_row)), dim3(NT), lds, st, a, rows,
                      wg_per_row);
   FDWT_CHECK_LAUNCH();
@@ -589,7 +802,7 @@ int dispatch_schain(const SChainArgs& a, int64_t rows, int wg, size_t lds, int d
 inline int compute_size(int dtype) { return dtype == FDWT_F64 ? 8 : 4; }
 
 inline bool valid_common(int64_t rows, int taps, int mode, int dtype) {
-  return rows >= 0 && taps >= 2 && taps % 2 == 0 && taps <= 4096 && mode >= 0 && mode <= 4 &&
+  return rows >= 0 && taps >= 2 && taps % 2 == 0 && taps <= MAX_TAPS && mode >= 0 && mode <= 4 &&
          dtype >= 0 && dtype <= 3;
 }
 
@@ -616,10 +829,11 @@ int extras_count(int64_t nc, int64_t m, int L, int off, int mode) {
 }
 
 void schain_caps(const int64_t* nc, const int64_t* n_out, int levels, int L, int off, int mode,
-                 int split, int* capA, int* capB, int* capE) {
-  const int64_t margin = 2 * (int64_t)L + 2 * VS + 8;
+                 int split, int* capA, int* capB, int* capE, int* capD) {
+  const int64_t zl = (L + 3) & ~3;
+  const int64_t margin = zl + L + 2 * VS + 24;
   int64_t a, b = 0, e = 4;
-  if (split) a = split / 2 + margin + 8;
+  if (split) a = split / 2 + margin + 16;
   else a = nc[0] + margin;
   for (int l = 0; l < levels; ++l) {
     e = std::max<int64_t>(e, extras_count(nc[l], n_out[l], L, off, mode));
@@ -631,6 +845,7 @@ void schain_caps(const int64_t* nc, const int64_t* n_out, int levels, int L, int
   *capA = (int)((a + 3) & ~3);
   *capB = (int)((b + 3) & ~3);
   *capE = (int)((e + 3) & ~3);
+  *capD = (int)((PS + L / 2 + 8 + 3) & ~3);
 }
 
 }  // namespace
@@ -742,13 +957,16 @@ extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* detai
     a.split = (int)per;
     wg = (int)cdiv(m, per);
   }
-  int capA, capB, capE;
-  schain_caps(nc, n_out, levels, taps, off, mode, a.split, &capA, &capB, &capE);
+  int capA, capB, capE, capD;
+  schain_caps(nc, n_out, levels, taps, off, mode, a.split, &capA, &capB, &capE, &capD);
   a.capA = capA;
   a.capB = capB;
   a.capE = capE;
+  a.capD = capD;
   const int cs = compute_size(dtype);
-  const size_t lds = (size_t)(capA + capB + capE + 2 * taps + 4) * cs;
+  // A, B, E, ET (ints), F, D, taps
+  const size_t lds = (size_t)(capA + capB + capE + (2 * capE + 8) + capD + 2 * taps + 4) * cs +
+                     (size_t)capE * 4;
   if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
   if (rows * wg > INT32_MAX) return FDWT_ERR_ARG;
   return dispatch_schain(a, rows, wg, lds, dtype, static_cast<hipStream_t>(stream));

@@ -49,12 +49,10 @@ def _analysis(x2, h0, h1, mode, off, n_out):
     y0 = torch.empty((R, n_out), device=x2.device, dtype=x2.dtype)
     y1 = torch.empty_like(y0)
     if R:
-        L = _lib.lib()
-        with torch.cuda.device(x2.device):
-            _lib.check(L.fdwt_dwt_analysis(
-                _lib.ptr(x2), _lib.ptr(y0), _lib.ptr(y1), _lib.ptr(h0), _lib.ptr(h1), R, n,
-                n_out, h0.numel(), mode, off, _lib.dtype_code(x2.dtype), _lib.stream(x2.device)),
-                "fdwt_dwt_analysis")
+        _lib.launch("fdwt_dwt_analysis", x2.device,
+                    _lib.ptr(x2), _lib.ptr(y0), _lib.ptr(y1), _lib.ptr(h0), _lib.ptr(h1), R, n,
+                    n_out, h0.numel(), mode, off, _lib.dtype_code(x2.dtype),
+                    _lib.stream(x2.device))
     return y0, y1
 
 
@@ -62,12 +60,9 @@ def _synthesis(a2, d2, h0, h1, mode, off, n, R, dtype, device):
     y = torch.empty((R, n), device=device, dtype=dtype)
     if R:
         nc = (a2 if a2 is not None else d2).shape[-1]
-        L = _lib.lib()
-        with torch.cuda.device(device):
-            _lib.check(L.fdwt_dwt_synthesis(
-                _lib.ptr(a2), _lib.ptr(d2), _lib.ptr(y), _lib.ptr(h0), _lib.ptr(h1), R, nc, n,
-                h0.numel(), mode, off, _lib.dtype_code(dtype), _lib.stream(device)),
-                "fdwt_dwt_synthesis")
+        _lib.launch("fdwt_dwt_synthesis", device,
+                    _lib.ptr(a2), _lib.ptr(d2), _lib.ptr(y), _lib.ptr(h0), _lib.ptr(h1), R, nc, n,
+                    h0.numel(), mode, off, _lib.dtype_code(dtype), _lib.stream(device))
     return y
 
 
@@ -95,13 +90,11 @@ def _analysis_chain(x2, h0, h1, mode, off, n_in, n_out):
         outs = [torch.empty((R, n_out[k]), device=x2.device, dtype=x2.dtype) for k in range(l, J)]
         approx = torch.empty((R, n_out[J - 1]), device=x2.device, dtype=x2.dtype)
         if R:
-            Lb = _lib.lib()
-            with torch.cuda.device(x2.device):
-                _lib.check(Lb.fdwt_analysis_chain(
-                    _lib.ptr(cur), _lib.ptr_array(outs), _lib.ptr(approx), _lib.ptr(h0),
-                    _lib.ptr(h1), R, _lib.i64_array(n_in[l:]), _lib.i64_array(n_out[l:]), J - l,
-                    taps, mode, off, _lib.dtype_code(x2.dtype), _lib.stream(x2.device)),
-                    "fdwt_analysis_chain")
+            _lib.launch("fdwt_analysis_chain", x2.device,
+                        _lib.ptr(cur), _lib.ptr_array(outs), _lib.ptr(approx), _lib.ptr(h0),
+                        _lib.ptr(h1), R, _lib.i64_array(n_in[l:]), _lib.i64_array(n_out[l:]),
+                        J - l, taps, mode, off, _lib.dtype_code(x2.dtype),
+                        _lib.stream(x2.device))
         details[l:] = outs
         cur = approx
     return details, cur
@@ -120,13 +113,11 @@ def _synthesis_chain(a2, ds, h0, h1, mode, off, nc, n_out, R, dtype, device):
     if k_end >= 1:
         cur = torch.empty((R, n_out[k_end - 1]), device=device, dtype=dtype)
         if R:
-            Lb = _lib.lib()
-            with torch.cuda.device(device):
-                _lib.check(Lb.fdwt_synthesis_chain(
-                    _lib.ptr(a2), _lib.ptr_array(ds[:k_end]), _lib.ptr(cur), _lib.ptr(h0),
-                    _lib.ptr(h1), R, _lib.i64_array(nc[:k_end]), _lib.i64_array(n_out[:k_end]),
-                    k_end, taps, mode, off, _lib.dtype_code(dtype), _lib.stream(device)),
-                    "fdwt_synthesis_chain")
+            _lib.launch("fdwt_synthesis_chain", device,
+                        _lib.ptr(a2), _lib.ptr_array(ds[:k_end]), _lib.ptr(cur), _lib.ptr(h0),
+                        _lib.ptr(h1), R, _lib.i64_array(nc[:k_end]),
+                        _lib.i64_array(n_out[:k_end]), k_end, taps, mode, off,
+                        _lib.dtype_code(dtype), _lib.stream(device))
     for k in range(k_end, K):
         a = cur[:, :nc[k]].contiguous()
         cur = _synthesis(a, ds[k], h0, h1, mode, off, n_out[k], R, dtype, device)
