@@ -97,6 +97,109 @@ int fdwt_synthesis_chain(const void* approx, const void* const* details, void* o
  * filter length and dtype; longer rows must first be reduced with fdwt_dwt_analysis. */
 int64_t fdwt_chain_max_length(int32_t taps, int32_t dtype);
 
+/* ---------------------------------------------------------------- Morlet CWT pyramid
+ *
+ * One octave ("stage") of the pyramid convolves a chain signal x_j (rows, n_in) with
+ * n_scales Morlet filters dilated by dil = 2^j:
+ *     W_s[r, n] = sum_{t=-half}^{half} H_s[c + t] * x_j[r, n + x_off - dil * t]
+ * Filters are given as a tap table taps[s][t][ch] = H_{s,ch}[c + t], t = 0..half, ch = re
+ * (and im when channels == 2); real parts must be even and imaginary parts odd around c, as
+ * every Morlet filter is.  support[s] (non-decreasing) bounds the non-zero taps of scale s,
+ * chan[s] is its output channel.  support / chan are host arrays of n_scales entries
+ * (n_scales <= FDWT_CWT_MAX_SCALES).  Compute dtypes: FDWT_F32 or FDWT_F64.
+ */
+#define FDWT_CWT_MAX_SCALES 64
+
+/* replaces the half-band launcher `halfband(x, taps, y, off, dil, transpose, accumulate)`
+ * (src/fdwt/kernels/conv.py:411-430):
+ *   y[r, n] (+)= taps[0] x[r, n + b] + sum_{t odd <= c} taps[t] (x[r, n + b - dil t] + x[r, n + b + dil t])
+ * with b = off - dil * c (forward) or dil * c - off (transpose); x is zero outside [0, n_in). */
+int fdwt_halfband(const void* x, const void* taps, void* y, int64_t rows, int64_t n_in,
+                  int64_t n_out, int32_t c, int64_t b, int32_t dil, int32_t accumulate,
+                  int32_t dtype, void* stream);
+
+/* replaces `forward(x, hT, kb, cmap, y, off, dil, block_s)` (conv.py:306-329): writes
+ * y[r, chan[s], n, ch] (y: (rows, s_total, n_out, channels), interleaved re / im). */
+int fdwt_morlet_forward(const void* x, const void* taps, void* y, int64_t rows, int64_t n_in,
+                        int64_t n_out, int64_t x_off, int32_t n_scales, int32_t half,
+                        const int32_t* support, const int32_t* chan, int32_t dil,
+                        int32_t channels, int32_t s_total, int32_t dtype, void* stream);
+
+/* replaces `backward_x(g, h, kf, cmap, gx, off, dil, accumulate)` (conv.py:345-369): the
+ * adjoint of fdwt_morlet_forward, gx (rows, n_in) (+)= A^T g with g (rows, g_scales, n_out,
+ * channels) read at channels chan[s]. */
+int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx, int64_t rows,
+                           int64_t n_in, int64_t n_out, int64_t x_off, int32_t n_scales,
+                           int32_t half, const int32_t* support, const int32_t* chan,
+                           int32_t dil, int32_t channels, int32_t g_scales, int32_t accumulate,
+                           int32_t dtype, void* stream);
+
+/* replaces `backward_h(x, g, kb, cmap, off, dil, K, block_s)` (conv.py:372-408): gradient of
+ * every tap, gh[s][k][ch] (+)= sum_{r,n} g[r, chan[s], n, ch] x[r, n + x_off - dil (k - half)],
+ * k = 0..2 half; gh: (n_scales, 2 half + 1, channels).  Deterministic: per-workgroup partial
+ * sums go to the caller's workspace (fdwt_morlet_backward_h_workspace elements), then one
+ * fixed-order reduction. */
+int64_t fdwt_morlet_backward_h_workspace(int64_t rows, int64_t n_out, int32_t n_scales,
+                                         int32_t half, int32_t channels);
+int fdwt_morlet_backward_h(const void* x, const void* g, void* workspace,
+                           int64_t workspace_elems, void* gh, int64_t rows, int64_t n_in,
+                           int64_t n_out, int64_t x_off, int32_t n_scales, int32_t half,
+                           const int32_t* support, const int32_t* chan, int32_t dil,
+                           int32_t channels, int32_t g_scales, int32_t accumulate,
+                           int32_t dtype, void* stream);
+
+/* Fused scalogram mix, replacing `mix_forward` / `mix_backward` (src/fdwt/kernels/mix.py:74-108):
+ *   forward   y[r, n] (+)= sum_s a[d, chan[s]] |W_s| + b[d, chan[s]] Re W_s,  d = (r + row0) % d_dim
+ *   backward  gw[r, s, n, ch] = dL/dW_s for the stage (gw: (rows, n_scales, n_out, channels)),
+ *             and per-(row, tile) partial sums (sum gy |W_s|, sum gy Re W_s) in the workspace,
+ *             laid out (rows, tiles, n_scales, 2); fdwt_mix_workspace gives its size.
+ * a, b: (d_dim, s_total) compute dtype.  The scalogram is never written to memory. */
+int64_t fdwt_mix_workspace(int64_t rows, int64_t n_out, int32_t n_scales);
+int fdwt_mix_forward(const void* x, const void* taps, const void* a, const void* b, void* y,
+                     int64_t rows, int64_t n_in, int64_t n_out, int64_t x_off,
+                     int32_t n_scales, int32_t half, const int32_t* support,
+                     const int32_t* chan, int32_t dil, int32_t channels, int32_t s_total,
+                     int32_t d_dim, int64_t row0, int32_t accumulate, int32_t dtype,
+                     void* stream);
+int fdwt_mix_backward(const void* x, const void* taps, const void* a, const void* b,
+                      const void* gy, void* gw, void* workspace, int64_t workspace_elems,
+                      int64_t rows, int64_t n_in, int64_t n_out, int64_t x_off,
+                      int32_t n_scales, int32_t half, const int32_t* support,
+                      const int32_t* chan, int32_t dil, int32_t channels, int32_t s_total,
+                      int32_t d_dim, int64_t row0, int32_t dtype, void* stream);
+
+/* out[o] (+)= sum over the rows * per_row items of partial[item * n_el + o], in a fixed
+ * order (deterministic counterpart of the reference's atomic accumulations). */
+int fdwt_reduce_rows(const void* partial, void* out, int64_t rows, int64_t per_row,
+                     int64_t n_el, int64_t stride_row, int32_t accumulate, int32_t dtype,
+                     void* stream);
+
+/* Spectral softmax stage, replacing `forward_stage` / `backward_stage`
+ * (src/fdwt/kernels/softmax.py:195-210).  a_f = |W_f| * inv_tau; V is per channel
+ * ((nch, v_s_total), row r uses V[(r + row0) % nch]) or per position ((G, v_s_total, n_out),
+ * row r uses V[(r + row0) / nch]).
+ *   forward  folds the stage into the online softmax state (m, l, num), each (rows, n_out);
+ *            first = no state yet; last = write num / l (the output) into num.
+ *   backward p = exp(a - m) / l, gp = gy p, writes gw (rows, n_scales, n_out, 2) =
+ *            gp (V - out) inv_tau W / |W| and dL/dV partials in the workspace: per channel
+ *            (rows, tiles, n_scales) sums over positions, per position (rows, n_scales, n_out)
+ *            (fdwt_softmax_workspace elements). */
+int fdwt_softmax_forward(const void* x, const void* taps, const void* v, int32_t v_per_position,
+                         int64_t v_s_total, int32_t nch, void* m, void* l, void* num,
+                         int64_t rows, int64_t n_in, int64_t n_out, int64_t x_off,
+                         int32_t n_scales, int32_t half, const int32_t* support,
+                         const int32_t* chan, int32_t dil, double inv_tau, int32_t first,
+                         int32_t last, int32_t dtype, void* stream);
+int64_t fdwt_softmax_workspace(int64_t rows, int64_t n_out, int32_t n_scales,
+                               int32_t v_per_position);
+int fdwt_softmax_backward(const void* x, const void* taps, const void* v,
+                          int32_t v_per_position, int64_t v_s_total, int32_t nch, int64_t row0,
+                          const void* m, const void* l, const void* out, const void* gy,
+                          void* gw, void* workspace, int64_t workspace_elems, int64_t rows,
+                          int64_t n_in, int64_t n_out, int64_t x_off, int32_t n_scales,
+                          int32_t half, const int32_t* support, const int32_t* chan,
+                          int32_t dil, double inv_tau, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

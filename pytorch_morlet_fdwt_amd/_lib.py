@@ -26,7 +26,8 @@ _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
 _PP = ctypes.POINTER(ctypes.c_void_p)
 _PI64 = ctypes.POINTER(ctypes.c_int64)
-_PF32 = ctypes.POINTER(ctypes.c_float)
+_PI32 = ctypes.POINTER(ctypes.c_int32)
+_DBL = ctypes.c_double
 
 # name -> argument types (restype int unless listed in _RESTYPE)
 SIGNATURES = {
@@ -39,9 +40,31 @@ SIGNATURES = {
     "fdwt_synthesis_chain": [_P, _PP, _P, _P, _P, _I64, _PI64, _PI64, _I32, _I32, _I32, _I32,
                              _I32, _P],
     "fdwt_chain_max_length": [_I32, _I32],
+    "fdwt_halfband": [_P, _P, _P, _I64, _I64, _I64, _I32, _I64, _I32, _I32, _I32, _P],
+    "fdwt_morlet_forward": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _PI32, _PI32, _I32,
+                            _I32, _I32, _I32, _P],
+    "fdwt_morlet_backward_x": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _PI32, _PI32,
+                               _I32, _I32, _I32, _I32, _I32, _P],
+    "fdwt_morlet_backward_h_workspace": [_I64, _I64, _I32, _I32, _I32],
+    "fdwt_morlet_backward_h": [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _I32, _PI32,
+                               _PI32, _I32, _I32, _I32, _I32, _I32, _P],
+    "fdwt_mix_workspace": [_I64, _I64, _I32],
+    "fdwt_mix_forward": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _PI32, _PI32,
+                         _I32, _I32, _I32, _I32, _I64, _I32, _I32, _P],
+    "fdwt_mix_backward": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+                          _PI32, _PI32, _I32, _I32, _I32, _I32, _I64, _I32, _P],
+    "fdwt_reduce_rows": [_P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _P],
+    "fdwt_softmax_forward": [_P, _P, _P, _I32, _I64, _I32, _P, _P, _P, _I64, _I64, _I64, _I64,
+                             _I32, _I32, _PI32, _PI32, _I32, _DBL, _I32, _I32, _I32, _P],
+    "fdwt_softmax_workspace": [_I64, _I64, _I32, _I32],
+    "fdwt_softmax_backward": [_P, _P, _P, _I32, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _I64,
+                              _I64, _I64, _I64, _I64, _I32, _I32, _PI32, _PI32, _I32, _DBL,
+                              _I32, _P],
 }
 _RESTYPE = {"fdwt_error_string": ctypes.c_char_p, "fdwt_version": ctypes.c_char_p,
-            "fdwt_chain_max_length": ctypes.c_int64}
+            "fdwt_chain_max_length": ctypes.c_int64,
+            "fdwt_morlet_backward_h_workspace": ctypes.c_int64,
+            "fdwt_mix_workspace": ctypes.c_int64, "fdwt_softmax_workspace": ctypes.c_int64}
 
 
 def library_path() -> str:

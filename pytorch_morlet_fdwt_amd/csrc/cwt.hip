@@ -1,0 +1,921 @@
+// Morlet CWT pyramid kernels for gfx950: half-band chain step, Morlet filter bank (forward,
+// adjoint, filter gradient), and the fused scalogram consumers (mix, spectral softmax).
+//
+// One octave ("stage") of the pyramid convolves the chain signal x_j with S_j Morlet
+// filters dilated by dil = 2^j (reference: src/fdwt/kernels/conv.py:38-134, cwt.py:213-244):
+//     W_s[n] = sum_{t=-half}^{half} H_s[c + t] x_j[n + x_off - dil t]
+// Morlet filters are even (real part) and odd (imaginary part) around their centre c
+// (cwt.py:194-203), so with n0 = n + x_off
+//     Re W_s[n] = h_s[0] x[n0] + sum_{t>=1} h_s[t] (x[n0 - dil t] + x[n0 + dil t])
+//     Im W_s[n] =                sum_{t>=1} g_s[t] (x[n0 - dil t] - x[n0 + dil t])
+// with taps h_s[t] = Re H_s[c + t], g_s[t] = Im H_s[c + t].  The sums and differences of a
+// tap pair are formed once per position and shared by every scale of the stage, halving
+// the multiplies of a direct convolution.  The taps are passed as a compact table
+// taps[s][t][ch] (t = 0..half, ch = re / im).
+//
+// Design: a workgroup owns one row and a tile of TT output positions; the tile of x_j it
+// needs (TT + 2 dil half samples) is staged in LDS by coalesced loads; thread i handles
+// positions n0 + i + NT v (v < V), so LDS reads of neighbouring lanes are neighbouring
+// words (no bank conflicts) and every output store is coalesced.  Scales are processed in
+// groups of SG with 2 V SG accumulators in registers.
+#include <algorithm>
+#include <type_traits>
+
+#include "common.h"
+
+namespace fdwt {
+namespace {
+
+constexpr int NT = 256;
+constexpr int V = 4;
+constexpr int TT = NT * V;        // output positions per workgroup
+constexpr int SG = 8;             // scales per register group
+constexpr int MAXS = FDWT_CWT_MAX_SCALES;
+
+struct Stage {
+  const void* x;     // (rows, n_in) chain signal of the stage
+  const void* taps;  // (n_scales, half + 1, C) compute dtype
+  int64_t n_in, n_out, x_off;
+  int32_t n_scales, half, dil, C;
+  int32_t sup[MAXS];   // per-scale half support (taps t > sup[s] are zero)
+  int32_t chan[MAXS];  // global scale index of each local scale
+};
+
+template <typename T>
+__device__ inline T load_clamped(const T* __restrict__ p, int64_t i, int64_t n) {
+  const T w = p[min(max(i, (int64_t)0), n - 1)];
+  return (i >= 0 && i < n) ? w : T(0);
+}
+
+// Stage x[row][p0 .. p0 + span) into X (zero outside [0, n)).
+template <typename T>
+__device__ inline void stage_row(T* X, const T* __restrict__ xrow, int64_t p0, int span,
+                                 int64_t n) {
+  for (int k = threadIdx.x; k < span; k += NT) X[k] = load_clamped(xrow, p0 + k, n);
+}
+
+// Scalogram of positions tid + NT v of the tile for the scale group [s0, s0 + ns), from the
+// staged tile X whose element ci + dil * half corresponds to tile position ci.
+template <typename T, bool CPLX>
+__device__ inline void bank_group(const T* __restrict__ X, const T* __restrict__ taps, int half,
+                                  int dil, int s0, int ns, int tmax, T (&re)[V][SG],
+                                  T (&im)[V][SG]) {
+  constexpr int C = CPLX ? 2 : 1;
+  const int tid = threadIdx.x;
+  const int base = tid + dil * half;
+  T xc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) xc[v] = X[base + NT * v];
+#pragma unroll
+  for (int s = 0; s < SG; ++s) {
+    const T h0 = s < ns ? taps[((s0 + s) * (half + 1)) * C] : T(0);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      re[v][s] = h0 * xc[v];
+      im[v][s] = T(0);
+    }
+  }
+  for (int t = 1; t <= tmax; ++t) {
+    T ps[V], ms[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const T a = X[base + NT * v - dil * t];
+      const T b = X[base + NT * v + dil * t];
+      ps[v] = a + b;
+      ms[v] = a - b;
+    }
+#pragma unroll
+    for (int s = 0; s < SG; ++s) {
+      if (s < ns) {
+        const T* tp = taps + ((s0 + s) * (half + 1) + t) * C;
+        const T hr = tp[0];
+#pragma unroll
+        for (int v = 0; v < V; ++v) re[v][s] = fma(hr, ps[v], re[v][s]);
+        if (CPLX) {
+          const T hi = tp[1];
+#pragma unroll
+          for (int v = 0; v < V; ++v) im[v][s] = fma(hi, ms[v], im[v][s]);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ bank forward
+template <typename T, bool CPLX>
+__global__ void __launch_bounds__(NT) morlet_forward_kernel(Stage st, T* __restrict__ y,
+                                                            int s_total, int tiles) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* X = reinterpret_cast<T*>(smem_raw);
+  constexpr int C = CPLX ? 2 : 1;
+  const int64_t row = blockIdx.x / tiles;
+  const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
+  const int span = TT + 2 * st.dil * st.half;
+  const T* xrow = static_cast<const T*>(st.x) + row * st.n_in;
+  stage_row(X, xrow, n0 + st.x_off - (int64_t)st.dil * st.half, span, st.n_in);
+  __syncthreads();
+  const T* taps = static_cast<const T*>(st.taps);
+  for (int s0 = 0; s0 < st.n_scales; s0 += SG) {
+    const int ns = min(SG, st.n_scales - s0);
+    T re[V][SG], im[V][SG];
+    bank_group<T, CPLX>(X, taps, st.half, st.dil, s0, ns, st.sup[s0 + ns - 1], re, im);
+#pragma unroll
+    for (int s = 0; s < SG; ++s) {
+      if (s >= ns) break;
+      T* yrow = y + ((row * s_total + st.chan[s0 + s]) * st.n_out) * C;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int64_t n = n0 + threadIdx.x + NT * v;
+        if (n < st.n_out) {
+          if (CPLX) {
+            typedef T v2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<v2*>(yrow + 2 * n) = v2{re[v][s], im[v][s]};
+          } else {
+            yrow[n] = re[v][s];
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ bank adjoint (grad x)
+// gx[p] (+)= sum_s [h_s[0] g_re[q] + sum_t h_s[t] (g_re[q + dil t] + g_re[q - dil t])
+//                                  + g_s[t] (g_im[q + dil t] - g_im[q - dil t])],  q = p - x_off
+// g: (rows, g_scales, n_out, C) with local scale s at channel chan[s].
+template <typename T, bool CPLX>
+__global__ void __launch_bounds__(NT) morlet_backward_x_kernel(Stage st, const T* __restrict__ g,
+                                                               T* __restrict__ gx, int g_scales,
+                                                               int tiles, int accumulate) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* G = reinterpret_cast<T*>(smem_raw);  // one scale: span x C (interleaved)
+  constexpr int C = CPLX ? 2 : 1;
+  const int64_t row = blockIdx.x / tiles;
+  const int64_t p0 = (int64_t)(blockIdx.x % tiles) * TT;
+  const int half = st.half, dil = st.dil;
+  const int span = TT + 2 * dil * half;
+  const int64_t q0 = p0 - st.x_off - (int64_t)dil * half;  // g position of G[0]
+  const T* taps = static_cast<const T*>(st.taps);
+  const int tid = threadIdx.x;
+  T acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = T(0);
+  for (int s = 0; s < st.n_scales; ++s) {
+    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out) * C;
+    __syncthreads();
+    for (int k = tid; k < span * C; k += NT) {
+      const int64_t q = q0 + k / C;
+      const T w = grow[min(max(q, (int64_t)0), st.n_out - 1) * C + (k % C)];
+      G[k] = (q >= 0 && q < st.n_out) ? w : T(0);
+    }
+    __syncthreads();
+    const int tmax = st.sup[s];
+    const T* tp = taps + s * (half + 1) * C;
+    const int base = tid + dil * half;
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = fma(tp[0], G[(base + NT * v) * C], acc[v]);
+    for (int t = 1; t <= tmax; ++t) {
+      const T hr = tp[t * C];
+      const T hi = CPLX ? tp[t * C + 1] : T(0);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int iu = (base + NT * v + dil * t) * C;
+        const int id = (base + NT * v - dil * t) * C;
+        acc[v] = fma(hr, G[iu] + G[id], acc[v]);
+        if (CPLX) acc[v] = fma(hi, G[iu + 1] - G[id + 1], acc[v]);
+      }
+    }
+  }
+  T* gxrow = gx + row * st.n_in;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t p = p0 + tid + NT * v;
+    if (p < st.n_in) gxrow[p] = accumulate ? gxrow[p] + acc[v] : acc[v];
+  }
+}
+
+// ------------------------------------------------------------------ filter gradient
+// Partial sums per workgroup of  gh[s][k][ch] = sum_n g[s, n, ch] x[n + x_off - dil (k - half)]
+// for k = 0 .. 2 half (every tap, no symmetry assumed); partial: (blocks, n_scales, 2 half + 1, C)
+template <typename T, bool CPLX>
+__global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T* __restrict__ g,
+                                                               T* __restrict__ partial,
+                                                               int g_scales, int tiles) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  constexpr int C = CPLX ? 2 : 1;
+  T* X = reinterpret_cast<T*>(smem_raw);
+  const int half = st.half, dil = st.dil;
+  const int span = TT + 2 * dil * half;
+  T* G = X + ((span + 3) & ~3);  // one scale of g: TT x C
+  const int64_t row = blockIdx.x / tiles;
+  const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
+  const int tid = threadIdx.x;
+  const T* xrow = static_cast<const T*>(st.x) + row * st.n_in;
+  stage_row(X, xrow, n0 + st.x_off - (int64_t)dil * half, span, st.n_in);
+  const int K = 2 * half + 1;
+  const int nvalid = (int)min((int64_t)TT, st.n_out - n0);
+  T* out = partial + (int64_t)blockIdx.x * st.n_scales * K * C;
+  for (int s = 0; s < st.n_scales; ++s) {
+    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out + n0) * C;
+    __syncthreads();
+    for (int k = tid; k < TT * C; k += NT) G[k] = (k / C < nvalid) ? grow[k] : T(0);
+    __syncthreads();
+    // thread -> (ch, tap k); positions looped
+    for (int w = tid; w < K * C; w += NT) {
+      const int k = w / C, ch = w % C;
+      const int sh = dil * (2 * half - k);  // X index of position i is i + sh
+      T a0 = T(0), a1 = T(0), a2 = T(0), a3 = T(0);
+      int i = 0;
+      for (; i + 4 <= nvalid; i += 4) {
+        a0 = fma(G[(i + 0) * C + ch], X[i + 0 + sh], a0);
+        a1 = fma(G[(i + 1) * C + ch], X[i + 1 + sh], a1);
+        a2 = fma(G[(i + 2) * C + ch], X[i + 2 + sh], a2);
+        a3 = fma(G[(i + 3) * C + ch], X[i + 3 + sh], a3);
+      }
+      for (; i < nvalid; ++i) a0 = fma(G[i * C + ch], X[i + sh], a0);
+      out[(s * K + k) * C + ch] = (a0 + a1) + (a2 + a3);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ half-band chain step
+// y[n] (+)= t0 x[n + b] + sum_{t odd <= c} taps[t] (x[n + b - dil t] + x[n + b + dil t])
+template <typename T>
+__global__ void __launch_bounds__(NT) halfband_kernel(const T* __restrict__ x,
+                                                      const T* __restrict__ taps,
+                                                      T* __restrict__ y, int64_t n_in,
+                                                      int64_t n_out, int c, int64_t b, int dil,
+                                                      int tiles, int accumulate) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* X = reinterpret_cast<T*>(smem_raw);
+  const int64_t row = blockIdx.x / tiles;
+  const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
+  const int span = TT + 2 * dil * c;
+  stage_row(X, x + row * n_in, n0 + b - (int64_t)dil * c, span, n_in);
+  __syncthreads();
+  const int tid = threadIdx.x;
+  const int base = tid + dil * c;
+  T acc[V];
+  const T t0 = taps[0];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = t0 * X[base + NT * v];
+  for (int t = 1; t <= c; t += 2) {
+    const T h = taps[t];
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      acc[v] = fma(h, X[base + NT * v - dil * t] + X[base + NT * v + dil * t], acc[v]);
+  }
+  T* yrow = y + row * n_out;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t n = n0 + tid + NT * v;
+    if (n < n_out) yrow[n] = accumulate ? yrow[n] + acc[v] : acc[v];
+  }
+}
+
+// ------------------------------------------------------------------ fused mix
+// forward:  y[r, n] (+)= sum_s a[d, chan_s] |W_s| + b[d, chan_s] Re W_s,  d = (r + row0) % D
+// backward: gw[r, s, n] = gy (a Re W / |W| + b,  a Im W / |W|)  (|W| = 0 -> 0), and per
+//           workgroup partial sums (sum gy |W|, sum gy Re W) per local scale.
+template <typename T, bool CPLX, bool GRAD>
+__global__ void __launch_bounds__(NT) mix_kernel(Stage st, const T* __restrict__ a,
+                                                 const T* __restrict__ b, int s_total_w, int D,
+                                                 int64_t row0, T* __restrict__ y,
+                                                 const T* __restrict__ gy, T* __restrict__ gw,
+                                                 T* __restrict__ partial, int tiles,
+                                                 int accumulate) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  constexpr int C = CPLX ? 2 : 1;
+  T* X = reinterpret_cast<T*>(smem_raw);
+  const int half = st.half, dil = st.dil;
+  const int span = TT + 2 * dil * half;
+  T* red = X + ((span + 3) & ~3);  // NT / 64 waves x 2 partial sums
+  const int64_t row = blockIdx.x / tiles;
+  const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
+  const int tid = threadIdx.x;
+  stage_row(X, static_cast<const T*>(st.x) + row * st.n_in, n0 + st.x_off - (int64_t)dil * half,
+            span, st.n_in);
+  __syncthreads();
+  const int d = (int)((row + row0) % D);
+  const T* taps = static_cast<const T*>(st.taps);
+  T gyv[V], out[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t n = n0 + tid + NT * v;
+    out[v] = T(0);
+    gyv[v] = (GRAD && n < st.n_out) ? gy[row * st.n_out + n] : T(0);
+  }
+  for (int s0 = 0; s0 < st.n_scales; s0 += SG) {
+    const int ns = min(SG, st.n_scales - s0);
+    T re[V][SG], im[V][SG];
+    bank_group<T, CPLX>(X, taps, half, dil, s0, ns, st.sup[s0 + ns - 1], re, im);
+#pragma unroll
+    for (int s = 0; s < SG; ++s) {
+      if (s >= ns) break;
+      const int gs = st.chan[s0 + s];
+      const T av = a[d * s_total_w + gs];
+      const T bv = b[d * s_total_w + gs];
+      T sa = T(0), sb = T(0);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int64_t n = n0 + tid + NT * v;
+        const T rv = re[v][s], iv = im[v][s];
+        const T mag = CPLX ? sqrt(rv * rv + iv * iv) : fabs(rv);
+        if (!GRAD) {
+          out[v] = fma(av, mag, fma(bv, rv, out[v]));
+        } else if (n < st.n_out) {
+          const T inv = mag > T(0) ? T(1) / mag : T(0);
+          T* gwp = gw + ((row * st.n_scales + s0 + s) * st.n_out + n) * C;
+          if (CPLX) {
+            typedef T v2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<v2*>(gwp) = v2{gyv[v] * (av * rv * inv + bv), gyv[v] * (av * iv * inv)};
+          } else {
+            // real transform: |W| = |Re W|, d|W|/dRe W = sign
+            gwp[0] = gyv[v] * (av * rv * inv + bv);
+          }
+          sa = fma(gyv[v], mag, sa);
+          sb = fma(gyv[v], rv, sb);
+        }
+      }
+      if (GRAD) {
+        // workgroup sum of (sa, sb): wave reduction, then across the NT / 64 waves
+        for (int o = 32; o > 0; o >>= 1) {
+          sa += __shfl_xor(sa, o);
+          sb += __shfl_xor(sb, o);
+        }
+        __syncthreads();
+        if ((tid & 63) == 0) {
+          red[2 * (tid >> 6)] = sa;
+          red[2 * (tid >> 6) + 1] = sb;
+        }
+        __syncthreads();
+        if (tid == 0) {
+          T ta = T(0), tb = T(0);
+          for (int w = 0; w < NT / 64; ++w) {
+            ta += red[2 * w];
+            tb += red[2 * w + 1];
+          }
+          T* pp = partial + ((int64_t)blockIdx.x * st.n_scales + s0 + s) * 2;
+          pp[0] = ta;
+          pp[1] = tb;
+        }
+      }
+    }
+  }
+  if (!GRAD) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t n = n0 + tid + NT * v;
+      if (n < st.n_out) {
+        T* yp = y + row * st.n_out + n;
+        *yp = accumulate ? *yp + out[v] : out[v];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ spectral softmax
+// V values: per channel (v_pos = 0): V[(r + row0) % nch][chan_s]   (layout (nch, S_total))
+//           per position (v_pos = 1): V[(r + row0) / nch][chan_s][n] (layout (G, S_total, N))
+struct SoftArgs {
+  const void* v;
+  int64_t s_total;
+  int32_t nch;
+  int32_t v_pos;
+  int64_t row0;
+  double inv_tau;
+};
+
+template <typename T>
+__device__ inline T v_value(const SoftArgs& sa, const T* V, int64_t row, int gs, int64_t n,
+                            int64_t n_out) {
+  const int64_t r = row + sa.row0;
+  if (sa.v_pos) return V[((r / sa.nch) * sa.s_total + gs) * n_out + n];
+  return V[(r % sa.nch) * sa.s_total + gs];
+}
+
+// forward: fold the stage into the online softmax state (m, l, num) of every position;
+// first: no state yet (m = -inf, l = 0, num = 0); last: write out = num / l into `num`.
+template <typename T>
+__global__ void __launch_bounds__(NT) softmax_forward_kernel(Stage st, SoftArgs sa,
+                                                             T* __restrict__ m, T* __restrict__ l,
+                                                             T* __restrict__ num, int tiles,
+                                                             int first, int last) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* X = reinterpret_cast<T*>(smem_raw);
+  const int half = st.half, dil = st.dil;
+  const int span = TT + 2 * dil * half;
+  const int64_t row = blockIdx.x / tiles;
+  const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
+  const int tid = threadIdx.x;
+  stage_row(X, static_cast<const T*>(st.x) + row * st.n_in, n0 + st.x_off - (int64_t)dil * half,
+            span, st.n_in);
+  __syncthreads();
+  const T* Vp = static_cast<const T*>(sa.v);
+  const T inv_tau = T(sa.inv_tau);
+  T mm[V], ll[V], nn[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t n = n0 + tid + NT * v;
+    const int64_t idx = row * st.n_out + min(n, st.n_out - 1);
+    mm[v] = first ? -INFINITY : m[idx];
+    ll[v] = first ? T(0) : l[idx];
+    nn[v] = first ? T(0) : num[idx];
+  }
+  const T* taps = static_cast<const T*>(st.taps);
+  for (int s0 = 0; s0 < st.n_scales; s0 += SG) {
+    const int ns = min(SG, st.n_scales - s0);
+    T re[V][SG], im[V][SG];
+    bank_group<T, true>(X, taps, half, dil, s0, ns, st.sup[s0 + ns - 1], re, im);
+#pragma unroll
+    for (int s = 0; s < SG; ++s) {
+      if (s >= ns) break;
+      const int gs = st.chan[s0 + s];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int64_t n = min(n0 + tid + NT * v, st.n_out - 1);
+        const T av = sqrt(re[v][s] * re[v][s] + im[v][s] * im[v][s]) * inv_tau;
+        const T val = v_value(sa, Vp, row, gs, n, st.n_out);
+        const T mn = max(mm[v], av);
+        const T alpha = exp(mm[v] - mn);  // exp(-inf) = 0 on the first frequency
+        const T e = exp(av - mn);
+        ll[v] = fma(ll[v], alpha, e);
+        nn[v] = fma(nn[v], alpha, e * val);
+        mm[v] = mn;
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t n = n0 + tid + NT * v;
+    if (n < st.n_out) {
+      const int64_t idx = row * st.n_out + n;
+      m[idx] = mm[v];
+      l[idx] = ll[v];
+      num[idx] = last ? nn[v] / ll[v] : nn[v];
+    }
+  }
+}
+
+// backward: p = exp(|W|/tau - m) / l, gp = gy p;  gw = gp (V - out) / tau * W / |W|;
+// dL/dV partials: per channel, per workgroup and local scale sum_n gp (partial (blocks, S_j));
+// per position, gp itself (partial (rows, S_j, n_out)), reduced over channels afterwards.
+template <typename T>
+__global__ void __launch_bounds__(NT) softmax_backward_kernel(Stage st, SoftArgs sa,
+                                                              const T* __restrict__ m,
+                                                              const T* __restrict__ l,
+                                                              const T* __restrict__ out,
+                                                              const T* __restrict__ gy,
+                                                              T* __restrict__ gw,
+                                                              T* __restrict__ partial,
+                                                              int tiles) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* X = reinterpret_cast<T*>(smem_raw);
+  const int half = st.half, dil = st.dil;
+  const int span = TT + 2 * dil * half;
+  T* red = X + ((span + 3) & ~3);
+  const int64_t row = blockIdx.x / tiles;
+  const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
+  const int tid = threadIdx.x;
+  stage_row(X, static_cast<const T*>(st.x) + row * st.n_in, n0 + st.x_off - (int64_t)dil * half,
+            span, st.n_in);
+  __syncthreads();
+  const T* Vp = static_cast<const T*>(sa.v);
+  const T inv_tau = T(sa.inv_tau);
+  T mm[V], il[V], oo[V], gg[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t n = n0 + tid + NT * v;
+    const int64_t idx = row * st.n_out + min(n, st.n_out - 1);
+    const bool ok = n < st.n_out;
+    mm[v] = m[idx];
+    il[v] = T(1) / l[idx];
+    oo[v] = out[idx];
+    gg[v] = ok ? gy[idx] : T(0);
+  }
+  const T* taps = static_cast<const T*>(st.taps);
+  for (int s0 = 0; s0 < st.n_scales; s0 += SG) {
+    const int ns = min(SG, st.n_scales - s0);
+    T re[V][SG], im[V][SG];
+    bank_group<T, true>(X, taps, half, dil, s0, ns, st.sup[s0 + ns - 1], re, im);
+#pragma unroll
+    for (int s = 0; s < SG; ++s) {
+      if (s >= ns) break;
+      const int gs = st.chan[s0 + s];
+      T sv = T(0);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int64_t n = n0 + tid + NT * v;
+        const bool ok = n < st.n_out;
+        const int64_t nc = min(n, st.n_out - 1);
+        const T rv = re[v][s], iv = im[v][s];
+        const T mag = sqrt(rv * rv + iv * iv);
+        const T p = exp(mag * inv_tau - mm[v]) * il[v];
+        const T gp = ok ? gg[v] * p : T(0);
+        const T val = v_value(sa, Vp, row, gs, nc, st.n_out);
+        const T inv = mag > T(0) ? T(1) / mag : T(0);
+        const T coef = gp * (val - oo[v]) * inv_tau * inv;
+        if (ok) {
+          typedef T v2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<v2*>(gw + ((row * st.n_scales + s0 + s) * st.n_out + n) * 2) =
+              v2{coef * rv, coef * iv};
+          if (sa.v_pos) partial[(row * st.n_scales + s0 + s) * st.n_out + n] = gp;
+        }
+        sv += gp;
+      }
+      if (!sa.v_pos) {
+        for (int o = 32; o > 0; o >>= 1) sv += __shfl_xor(sv, o);
+        __syncthreads();
+        if ((tid & 63) == 0) red[tid >> 6] = sv;
+        __syncthreads();
+        if (tid == 0) {
+          T tsum = T(0);
+          for (int w = 0; w < NT / 64; ++w) tsum += red[w];
+          partial[(int64_t)blockIdx.x * st.n_scales + s0 + s] = tsum;
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ deterministic reductions
+// out[o] (+)= sum_{i < count} in[i * stride_i + o * stride_o] (fixed order), o < n_out_el
+template <typename T>
+__global__ void reduce_strided_kernel(const T* __restrict__ in, T* __restrict__ out, int64_t n,
+                                      int64_t count, int64_t stride_i, int64_t stride_o,
+                                      int accumulate) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= n) return;
+  T acc = T(0);
+  for (int64_t i = 0; i < count; ++i) acc += in[i * stride_i + o * stride_o];
+  out[o] = accumulate ? out[o] + acc : acc;
+}
+
+// ------------------------------------------------------------------ host helpers
+int fill_stage(Stage& st, const void* x, const void* taps, int64_t n_in, int64_t n_out,
+               int64_t x_off, int32_t n_scales, int32_t half, const int32_t* support,
+               const int32_t* chan, int32_t dil, int32_t channels) {
+  if (!x || !taps || n_in < 0 || n_out < 0 || n_scales < 1 || n_scales > MAXS || half < 0 ||
+      dil < 1 || !support || !chan || (channels != 1 && channels != 2))
+    return FDWT_ERR_ARG;
+  if ((int64_t)dil * half > (1 << 20)) return FDWT_ERR_TOO_LONG;
+  st.x = x;
+  st.taps = taps;
+  st.n_in = n_in;
+  st.n_out = n_out;
+  st.x_off = x_off;
+  st.n_scales = n_scales;
+  st.half = half;
+  st.dil = dil;
+  st.C = channels;
+  for (int s = 0; s < n_scales; ++s) {
+    if (support[s] < 0 || support[s] > half || chan[s] < 0) return FDWT_ERR_ARG;
+    if (s > 0 && support[s] < support[s - 1]) return FDWT_ERR_ARG;  // sorted by support
+    st.sup[s] = support[s];
+    st.chan[s] = chan[s];
+  }
+  return 0;
+}
+
+inline size_t tile_lds(const Stage& st, int cs, int extra_elems) {
+  const int64_t span = TT + 2 * (int64_t)st.dil * st.half;
+  return (size_t)(((span + 3) & ~3) + extra_elems) * cs;
+}
+
+template <typename K>
+inline bool allow_full_lds(K kernel) {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  return true;
+}
+
+template <typename K, typename... Args>
+int launch(K kernel, int64_t blocks, size_t lds, hipStream_t st, Args... args) {
+  if (blocks <= 0) return 0;
+  if (blocks > INT32_MAX) return FDWT_ERR_ARG;
+  if (lds > 160 * 1024) return FDWT_ERR_TOO_LONG;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(NT), lds, st, args...);
+  FDWT_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // namespace
+}  // namespace fdwt
+
+using namespace fdwt;
+
+#define FDWT_LDS_ONCE(K)                                   \
+  do {                                                     \
+    static const bool lds_ok_ = allow_full_lds(K);         \
+    (void)lds_ok_;                                         \
+  } while (0)
+
+extern "C" int fdwt_halfband(const void* x, const void* taps, void* y, int64_t rows,
+                             int64_t n_in, int64_t n_out, int32_t c, int64_t b, int32_t dil,
+                             int32_t accumulate, int32_t dtype, void* stream) {
+  if (!x || !taps || !y || rows < 0 || n_in < 1 || n_out < 0 || c < 0 || dil < 1 ||
+      (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  if (rows == 0 || n_out == 0) return 0;
+  const int tiles = (int)cdiv(n_out, TT);
+  const int64_t span = TT + 2 * (int64_t)dil * c;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FDWT_F32) {
+    auto k = halfband_kernel<float>;
+    FDWT_LDS_ONCE(k);
+    return launch(k, rows * tiles, (size_t)span * 4, st, (const float*)x, (const float*)taps,
+                  (float*)y, n_in, n_out, c, b, dil, tiles, accumulate);
+  }
+  auto k = halfband_kernel<double>;
+  FDWT_LDS_ONCE(k);
+  return launch(k, rows * tiles, (size_t)span * 8, st, (const double*)x, (const double*)taps,
+                (double*)y, n_in, n_out, c, b, dil, tiles, accumulate);
+}
+
+extern "C" int fdwt_morlet_forward(const void* x, const void* taps, void* y, int64_t rows,
+                                   int64_t n_in, int64_t n_out, int64_t x_off, int32_t n_scales,
+                                   int32_t half, const int32_t* support, const int32_t* chan,
+                                   int32_t dil, int32_t channels, int32_t s_total, int32_t dtype,
+                                   void* stream) {
+  Stage st;
+  int e = fill_stage(st, x, taps, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
+  if (e) return e;
+  if (!y || rows < 0 || s_total < n_scales || (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  for (int s = 0; s < n_scales; ++s)
+    if (chan[s] >= s_total) return FDWT_ERR_ARG;
+  if (rows == 0 || n_out == 0) return 0;
+  const int tiles = (int)cdiv(n_out, TT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int cs = dtype == FDWT_F64 ? 8 : 4;
+  const size_t lds = tile_lds(st, cs, 0);
+#define FWD(TYPE, CPLX)                                                                  \
+  do {                                                                                   \
+    auto k = morlet_forward_kernel<TYPE, CPLX>;                                          \
+    FDWT_LDS_ONCE(k);                                                                    \
+    return launch(k, rows * tiles, lds, hs, st, (TYPE*)y, (int)s_total, tiles);          \
+  } while (0)
+  if (dtype == FDWT_F32) {
+    if (channels == 2) FWD(float, true);
+    FWD(float, false);
+  }
+  if (channels == 2) FWD(double, true);
+  FWD(double, false);
+#undef FWD
+}
+
+extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx, int64_t rows,
+                                      int64_t n_in, int64_t n_out, int64_t x_off,
+                                      int32_t n_scales, int32_t half, const int32_t* support,
+                                      const int32_t* chan, int32_t dil, int32_t channels,
+                                      int32_t g_scales, int32_t accumulate, int32_t dtype,
+                                      void* stream) {
+  Stage st;
+  // the stage's x is unused here; pass g to satisfy the null check
+  int e = fill_stage(st, g, taps, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
+  if (e) return e;
+  if (!gx || rows < 0 || g_scales < 1 || (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  for (int s = 0; s < n_scales; ++s)
+    if (chan[s] >= g_scales) return FDWT_ERR_ARG;
+  if (rows == 0 || n_in == 0) return 0;
+  if (n_out == 0) return FDWT_ERR_ARG;
+  const int tiles = (int)cdiv(n_in, TT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int cs = dtype == FDWT_F64 ? 8 : 4;
+  const size_t lds = (size_t)((TT + 2 * (int64_t)dil * half) * channels + 4) * cs;
+#define BWX(TYPE, CPLX)                                                                     \
+  do {                                                                                      \
+    auto k = morlet_backward_x_kernel<TYPE, CPLX>;                                          \
+    FDWT_LDS_ONCE(k);                                                                       \
+    return launch(k, rows * tiles, lds, hs, st, (const TYPE*)g, (TYPE*)gx, (int)g_scales,    \
+                  tiles, (int)accumulate);                                                  \
+  } while (0)
+  if (dtype == FDWT_F32) {
+    if (channels == 2) BWX(float, true);
+    BWX(float, false);
+  }
+  if (channels == 2) BWX(double, true);
+  BWX(double, false);
+#undef BWX
+}
+
+extern "C" int64_t fdwt_morlet_backward_h_workspace(int64_t rows, int64_t n_out, int32_t n_scales,
+                                                    int32_t half, int32_t channels) {
+  const int64_t tiles = cdiv(n_out, TT);
+  return rows * tiles * (int64_t)n_scales * (2 * (int64_t)half + 1) * channels;
+}
+
+extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* workspace,
+                                      int64_t workspace_elems, void* gh, int64_t rows,
+                                      int64_t n_in, int64_t n_out, int64_t x_off,
+                                      int32_t n_scales, int32_t half, const int32_t* support,
+                                      const int32_t* chan, int32_t dil, int32_t channels,
+                                      int32_t g_scales, int32_t accumulate, int32_t dtype,
+                                      void* stream) {
+  Stage st;
+  int e = fill_stage(st, x, g, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
+  if (e) return e;
+  if (!workspace || !gh || rows < 0 || (dtype != FDWT_F32 && dtype != FDWT_F64)) return FDWT_ERR_ARG;
+  for (int s = 0; s < n_scales; ++s)
+    if (chan[s] >= g_scales) return FDWT_ERR_ARG;
+  const int64_t need = fdwt_morlet_backward_h_workspace(rows, n_out, n_scales, half, channels);
+  if (workspace_elems < need) return FDWT_ERR_ARG;
+  const int64_t K = 2 * (int64_t)half + 1;
+  const int64_t n_el = n_scales * K * channels;
+  if (rows == 0 || n_out == 0) return 0;
+  const int tiles = (int)cdiv(n_out, TT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int cs = dtype == FDWT_F64 ? 8 : 4;
+  const int64_t span = TT + 2 * (int64_t)dil * half;
+  const size_t lds = (size_t)(((span + 3) & ~3) + TT * channels) * cs;
+  const int64_t blocks = rows * tiles;
+  int rc;
+#define BWH(TYPE, CPLX)                                                                       \
+  do {                                                                                        \
+    auto k = morlet_backward_h_kernel<TYPE, CPLX>;                                            \
+    FDWT_LDS_ONCE(k);                                                                         \
+    rc = launch(k, blocks, lds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,      \
+                tiles);                                                                       \
+    if (rc) return rc;                                                                        \
+    return launch(reduce_strided_kernel<TYPE>, cdiv(n_el, NT), 0, hs, (const TYPE*)workspace, \
+                  (TYPE*)gh, n_el, blocks, n_el, (int64_t)1, (int)accumulate);                \
+  } while (0)
+  if (dtype == FDWT_F32) {
+    if (channels == 2) BWH(float, true);
+    BWH(float, false);
+  }
+  if (channels == 2) BWH(double, true);
+  BWH(double, false);
+#undef BWH
+}
+
+extern "C" int64_t fdwt_mix_workspace(int64_t rows, int64_t n_out, int32_t n_scales) {
+  return rows * cdiv(n_out, TT) * (int64_t)n_scales * 2;
+}
+
+extern "C" int fdwt_mix_forward(const void* x, const void* taps, const void* a, const void* b,
+                                void* y, int64_t rows, int64_t n_in, int64_t n_out,
+                                int64_t x_off, int32_t n_scales, int32_t half,
+                                const int32_t* support, const int32_t* chan, int32_t dil,
+                                int32_t channels, int32_t s_total, int32_t d_dim, int64_t row0,
+                                int32_t accumulate, int32_t dtype, void* stream) {
+  Stage st;
+  int e = fill_stage(st, x, taps, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
+  if (e) return e;
+  if (!a || !b || !y || rows < 0 || d_dim < 1 || row0 < 0 || (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  for (int s = 0; s < n_scales; ++s)
+    if (chan[s] >= s_total) return FDWT_ERR_ARG;
+  if (rows == 0 || n_out == 0) return 0;
+  const int tiles = (int)cdiv(n_out, TT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int cs = dtype == FDWT_F64 ? 8 : 4;
+  const size_t lds = tile_lds(st, cs, 16);
+#define MIXF(TYPE, CPLX)                                                                      \
+  do {                                                                                        \
+    auto k = mix_kernel<TYPE, CPLX, false>;                                                   \
+    FDWT_LDS_ONCE(k);                                                                         \
+    return launch(k, rows * tiles, lds, hs, st, (const TYPE*)a, (const TYPE*)b, (int)s_total,  \
+                  (int)d_dim, row0, (TYPE*)y, (const TYPE*)nullptr, (TYPE*)nullptr,           \
+                  (TYPE*)nullptr, tiles, (int)accumulate);                                    \
+  } while (0)
+  if (dtype == FDWT_F32) {
+    if (channels == 2) MIXF(float, true);
+    MIXF(float, false);
+  }
+  if (channels == 2) MIXF(double, true);
+  MIXF(double, false);
+#undef MIXF
+}
+
+extern "C" int fdwt_mix_backward(const void* x, const void* taps, const void* a, const void* b,
+                                 const void* gy, void* gw, void* workspace,
+                                 int64_t workspace_elems, int64_t rows, int64_t n_in,
+                                 int64_t n_out, int64_t x_off, int32_t n_scales, int32_t half,
+                                 const int32_t* support, const int32_t* chan, int32_t dil,
+                                 int32_t channels, int32_t s_total, int32_t d_dim, int64_t row0,
+                                 int32_t dtype, void* stream) {
+  Stage st;
+  int e = fill_stage(st, x, taps, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
+  if (e) return e;
+  if (!a || !b || !gy || !gw || !workspace || rows < 0 || d_dim < 1 || row0 < 0 ||
+      (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  for (int s = 0; s < n_scales; ++s)
+    if (chan[s] >= s_total) return FDWT_ERR_ARG;
+  if (workspace_elems < fdwt_mix_workspace(rows, n_out, n_scales)) return FDWT_ERR_ARG;
+  if (rows == 0 || n_out == 0) return 0;
+  const int tiles = (int)cdiv(n_out, TT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int cs = dtype == FDWT_F64 ? 8 : 4;
+  const size_t lds = tile_lds(st, cs, 16);
+  // gab receives the per-(row, tile) partial sums (blocks, n_scales, 2); the caller reduces
+  // rows sharing a weight row d with fdwt_reduce_rows (deterministic order)
+#define MIXB(TYPE, CPLX)                                                                      \
+  do {                                                                                        \
+    auto k = mix_kernel<TYPE, CPLX, true>;                                                    \
+    FDWT_LDS_ONCE(k);                                                                         \
+    return launch(k, rows * tiles, lds, hs, st, (const TYPE*)a, (const TYPE*)b, (int)s_total,  \
+                  (int)d_dim, row0, (TYPE*)nullptr, (const TYPE*)gy, (TYPE*)gw,               \
+                  (TYPE*)workspace, tiles, 0);                                                \
+  } while (0)
+  if (dtype == FDWT_F32) {
+    if (channels == 2) MIXB(float, true);
+    MIXB(float, false);
+  }
+  if (channels == 2) MIXB(double, true);
+  MIXB(double, false);
+#undef MIXB
+}
+
+extern "C" int fdwt_reduce_rows(const void* partial, void* out, int64_t rows, int64_t per_row,
+                                int64_t n_el, int64_t stride_row, int32_t accumulate,
+                                int32_t dtype, void* stream) {
+  // out[o] (+)= sum_{r < rows} sum_{j < per_row} partial[r * stride_row + j * n_el + o]
+  if (!partial || !out || rows < 0 || per_row < 0 || n_el < 0 ||
+      (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  if (n_el == 0) return 0;
+  if (stride_row != per_row * n_el) return FDWT_ERR_ARG;  // contiguous (rows x per_row) items
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (dtype == FDWT_F32)
+    return launch(reduce_strided_kernel<float>, cdiv(n_el, NT), 0, hs, (const float*)partial,
+                  (float*)out, n_el, rows * per_row, n_el, (int64_t)1, (int)accumulate);
+  return launch(reduce_strided_kernel<double>, cdiv(n_el, NT), 0, hs, (const double*)partial,
+                (double*)out, n_el, rows * per_row, n_el, (int64_t)1, (int)accumulate);
+}
+
+extern "C" int fdwt_softmax_forward(const void* x, const void* taps, const void* v,
+                                    int32_t v_per_position, int64_t v_s_total, int32_t nch,
+                                    void* m, void* l, void* num, int64_t rows, int64_t n_in,
+                                    int64_t n_out, int64_t x_off, int32_t n_scales, int32_t half,
+                                    const int32_t* support, const int32_t* chan, int32_t dil,
+                                    double inv_tau, int32_t first, int32_t last, int32_t dtype,
+                                    void* stream) {
+  Stage st;
+  int e = fill_stage(st, x, taps, n_in, n_out, x_off, n_scales, half, support, chan, dil, 2);
+  if (e) return e;
+  if (!v || !m || !l || !num || rows < 0 || nch < 1 || (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  for (int s = 0; s < n_scales; ++s)
+    if (chan[s] >= v_s_total) return FDWT_ERR_ARG;
+  if (rows == 0 || n_out == 0) return 0;
+  SoftArgs sa{v, v_s_total, nch, v_per_position ? 1 : 0, 0, inv_tau};
+  const int tiles = (int)cdiv(n_out, TT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int cs = dtype == FDWT_F64 ? 8 : 4;
+  const size_t lds = tile_lds(st, cs, 0);
+  if (dtype == FDWT_F32) {
+    auto k = softmax_forward_kernel<float>;
+    FDWT_LDS_ONCE(k);
+    return launch(k, rows * tiles, lds, hs, st, sa, (float*)m, (float*)l, (float*)num, tiles,
+                  (int)first, (int)last);
+  }
+  auto k = softmax_forward_kernel<double>;
+  FDWT_LDS_ONCE(k);
+  return launch(k, rows * tiles, lds, hs, st, sa, (double*)m, (double*)l, (double*)num, tiles,
+                (int)first, (int)last);
+}
+
+extern "C" int64_t fdwt_softmax_workspace(int64_t rows, int64_t n_out, int32_t n_scales,
+                                          int32_t v_per_position) {
+  if (v_per_position) return rows * (int64_t)n_scales * n_out;
+  return rows * cdiv(n_out, TT) * (int64_t)n_scales;
+}
+
+extern "C" int fdwt_softmax_backward(const void* x, const void* taps, const void* v,
+                                     int32_t v_per_position, int64_t v_s_total, int32_t nch,
+                                     int64_t row0, const void* m, const void* l, const void* out,
+                                     const void* gy, void* gw, void* workspace,
+                                     int64_t workspace_elems, int64_t rows, int64_t n_in,
+                                     int64_t n_out, int64_t x_off, int32_t n_scales, int32_t half,
+                                     const int32_t* support, const int32_t* chan, int32_t dil,
+                                     double inv_tau, int32_t dtype, void* stream) {
+  Stage st;
+  int e = fill_stage(st, x, taps, n_in, n_out, x_off, n_scales, half, support, chan, dil, 2);
+  if (e) return e;
+  if (!v || !m || !l || !out || !gy || !gw || !workspace || rows < 0 || nch < 1 || row0 < 0 ||
+      (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  for (int s = 0; s < n_scales; ++s)
+    if (chan[s] >= v_s_total) return FDWT_ERR_ARG;
+  if (workspace_elems < fdwt_softmax_workspace(rows, n_out, n_scales, v_per_position))
+    return FDWT_ERR_ARG;
+  if (rows == 0 || n_out == 0) return 0;
+  SoftArgs sa{v, v_s_total, nch, v_per_position ? 1 : 0, row0, inv_tau};
+  const int tiles = (int)cdiv(n_out, TT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int cs = dtype == FDWT_F64 ? 8 : 4;
+  const size_t lds = tile_lds(st, cs, 16);
+  if (dtype == FDWT_F32) {
+    auto k = softmax_backward_kernel<float>;
+    FDWT_LDS_ONCE(k);
+    return launch(k, rows * tiles, lds, hs, st, sa, (const float*)m, (const float*)l,
+                  (const float*)out, (const float*)gy, (float*)gw, (float*)workspace, tiles);
+  }
+  auto k = softmax_backward_kernel<double>;
+  FDWT_LDS_ONCE(k);
+  return launch(k, rows * tiles, lds, hs, st, sa, (const double*)m, (const double*)l,
+                (const double*)out, (const double*)gy, (double*)gw, (double*)workspace, tiles);
+}

@@ -541,7 +541,8 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
       const int idx = tid + k * NT;
       const int u = pbl + idx;
       T v = T(0);
-      if (dr && idx < dspan) {
+      // blocks of NT entirely outside the coefficients are skipped (block-uniform test)
+      if (dr && idx < dspan && pbl + k * NT < ncl && pbl + k * NT + NT > 0) {
         const T w = T(Storage<S>::load(dr, min(max(u, 0), ncl - 1)));
         v = (u >= 0 && u < ncl) ? w : T(0);
       }
