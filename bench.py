@@ -136,12 +136,102 @@ def cpu_baseline(rows=16, reps=3):
                       f"({t:.2f} s per step)"}
 
 
+ATT_SHAPE = (8, 4, 19, 30, 200)  # (B, H, C, T, D)
+FP32_PEAK = 157.3e12
+
+
+def attention_flops(m, R, N):
+    """Algorithmic FLOPs of one MorletAttention forward + backward (2 per real filter-tap
+    MAC, unfolded taps, half-band chain included): forward = chain + filter bank; backward =
+    chain recompute + bank recompute + grad-x + grad-h + transposed chain."""
+    plan = m.cwt.plan
+    bank = 0
+    for st in plan.stages:
+        for sup in st.support:
+            bank += 2 * 2 * (2 * sup + 1) * plan.channels * R * N
+    chain = 0
+    for j in range(plan.n_octaves - 1):
+        chain += 2 * (2 * plan.c_lp + 1) * R * (N + 2 * plan.margins[j + 1])
+    return 4 * bank + 3 * chain
+
+
+def attention_gpu(steps, warmup, dev):
+    import pytorch_morlet_fdwt_amd as fdwt
+    B, H, C, T, D = ATT_SHAPE
+    torch.manual_seed(2)
+    m = fdwt.MorletAttention(num_channels=C, hidden_dim=D).to(dev)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(*ATT_SHAPE, generator=g).to(dev).requires_grad_()
+    gy = torch.randn(*ATT_SHAPE, generator=torch.Generator().manual_seed(1)).to(dev)
+    params = [x] + list(m.parameters())
+
+    def step():
+        y = m(x)
+        torch.autograd.grad(y, params, gy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    R, N = B * H * C, T * D
+    fl = attention_flops(m, R, N)
+    tokens = B * C * T
+    return {"metric": "MorletAttention fwd+bwd tokens/s (B*C*T per step)",
+            "value": tokens / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms,
+            "config": {"shape_BHCTD": list(ATT_SHAPE), "freqs": "16 logspace(0, log10(40)) Hz",
+                       "fs": D, "learnable": True, "temperature": 1.0},
+            "roofline": {"bound": "valu", "achieved": fl / (ms * 1e-3) / 1e12,
+                         "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                         "frac": fl / (ms * 1e-3) / FP32_PEAK, "alg_flops": fl}}
+
+
+def attention_cpu(batch=1, reps=3):
+    """The oracle (reference CPU fallback restated, fp32) on a batch-`batch` sample."""
+    from oracle import cwt as O
+    import pytorch_morlet_fdwt_amd as fdwt
+    B, H, C, T, D = ATT_SHAPE
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    torch.manual_seed(2)
+    m = fdwt.MorletAttention(num_channels=C, hidden_dim=D)
+    plan = O.Plan(m.cwt.plan.scales, support_margin=1.25)
+    x = torch.randn(batch, H, C, T, D, generator=torch.Generator().manual_seed(0))
+    ls = m.cwt.log_scales.detach().clone().requires_grad_()
+    w0 = torch.tensor(6.0, requires_grad=True)
+    fw = m.freq_weight.detach().clone().requires_grad_()
+
+    def run():
+        xx = x.clone().requires_grad_()
+        Hf = plan.filters(ls.double().exp(), w0.double(), torch.float32)
+        y = O.attention(xx, plan, Hf, fw, 1.0)
+        torch.autograd.grad(y, [xx, ls, w0, fw], torch.ones_like(y))
+
+    run()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    return {"value": batch * C * T / t, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"B={batch} of {B} (shape {[batch, H, C, T, D]}), fp32, learnable scales "
+                      f"and w0, median of {reps} after 1 warm-up ({t:.2f} s per step)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy (HBM counter calibration)")
@@ -218,6 +308,11 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
     }
+    if not a.no_attention:
+        att = attention_gpu(max(3, a.steps // 2), a.warmup, dev)
+        if not a.no_cpu_baseline:
+            att["cpu_baseline"] = attention_cpu()
+        line["morlet_attention"] = att
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(a.cpu_rows)
     print(json.dumps(line))

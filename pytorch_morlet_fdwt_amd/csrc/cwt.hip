@@ -196,7 +196,13 @@ __global__ void __launch_bounds__(NT) morlet_backward_x_kernel(Stage st, const T
 
 // ------------------------------------------------------------------ filter gradient
 // Partial sums per workgroup of  gh[s][k][ch] = sum_n g[s, n, ch] x[n + x_off - dil (k - half)]
-// for k = 0 .. 2 half (every tap, no symmetry assumed); partial: (blocks, n_scales, 2 half + 1, C)
+// for k = 0 .. 2 half (every tap, no symmetry assumed).  Lane i of a wave handles positions
+// i, i + 64, ... of the tile (conflict-free LDS reads), KB taps at a time sharing each g
+// load; the 64 lanes are then summed with wave shuffles.  partial: (n_el, blocks) with
+// n_el = n_scales (2 half + 1) C, written transposed so that the final reduction reads
+// contiguous memory.
+constexpr int KB = 8;
+
 template <typename T, bool CPLX>
 __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T* __restrict__ g,
                                                                T* __restrict__ partial,
@@ -206,34 +212,45 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
   T* X = reinterpret_cast<T*>(smem_raw);
   const int half = st.half, dil = st.dil;
   const int span = TT + 2 * dil * half;
-  T* G = X + ((span + 3) & ~3);  // one scale of g: TT x C
+  T* G = X + ((span + 3) & ~3);  // one scale of g, de-interleaved: G[ch * TT + i]
   const int64_t row = blockIdx.x / tiles;
   const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
-  const int tid = threadIdx.x;
+  const int64_t nblocks = (int64_t)gridDim.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const T* xrow = static_cast<const T*>(st.x) + row * st.n_in;
   stage_row(X, xrow, n0 + st.x_off - (int64_t)dil * half, span, st.n_in);
   const int K = 2 * half + 1;
   const int nvalid = (int)min((int64_t)TT, st.n_out - n0);
-  T* out = partial + (int64_t)blockIdx.x * st.n_scales * K * C;
   for (int s = 0; s < st.n_scales; ++s) {
     const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out + n0) * C;
     __syncthreads();
-    for (int k = tid; k < TT * C; k += NT) G[k] = (k / C < nvalid) ? grow[k] : T(0);
+    for (int k = tid; k < TT * C; k += NT) {
+      const int i = k / C, ch = k % C;
+      G[ch * TT + i] = (i < nvalid) ? grow[k] : T(0);
+    }
     __syncthreads();
-    // thread -> (ch, tap k); positions looped
-    for (int w = tid; w < K * C; w += NT) {
-      const int k = w / C, ch = w % C;
-      const int sh = dil * (2 * half - k);  // X index of position i is i + sh
-      T a0 = T(0), a1 = T(0), a2 = T(0), a3 = T(0);
-      int i = 0;
-      for (; i + 4 <= nvalid; i += 4) {
-        a0 = fma(G[(i + 0) * C + ch], X[i + 0 + sh], a0);
-        a1 = fma(G[(i + 1) * C + ch], X[i + 1 + sh], a1);
-        a2 = fma(G[(i + 2) * C + ch], X[i + 2 + sh], a2);
-        a3 = fma(G[(i + 3) * C + ch], X[i + 3 + sh], a3);
+    for (int k0 = wave * KB; k0 < K; k0 += (NT / 64) * KB) {
+#pragma unroll
+      for (int ch = 0; ch < C; ++ch) {
+        T acc[KB];
+#pragma unroll
+        for (int b = 0; b < KB; ++b) acc[b] = T(0);
+        for (int i = lane; i < nvalid; i += 64) {
+          const T gv = G[ch * TT + i];
+#pragma unroll
+          for (int b = 0; b < KB; ++b) {
+            const int k = min(k0 + b, K - 1);  // X index of position i is i + dil (2 half - k)
+            acc[b] = fma(gv, X[i + dil * (2 * half - k)], acc[b]);
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+          T v = acc[b];
+          for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+          if (lane == 0 && k0 + b < K)
+            partial[((int64_t)(s * K + k0 + b) * C + ch) * nblocks + blockIdx.x] = v;
+        }
       }
-      for (; i < nvalid; ++i) a0 = fma(G[i * C + ch], X[i + sh], a0);
-      out[(s * K + k) * C + ch] = (a0 + a1) + (a2 + a3);
     }
   }
 }
@@ -551,6 +568,27 @@ __global__ void reduce_strided_kernel(const T* __restrict__ in, T* __restrict__ 
   out[o] = accumulate ? out[o] + acc : acc;
 }
 
+// out[o] (+)= sum_{i < count} in[o * count + i]: one workgroup per output, fixed order
+// (per-thread strided sums, then a fixed shuffle / LDS tree).
+template <typename T>
+__global__ void __launch_bounds__(NT) reduce_cols_kernel(const T* __restrict__ in,
+                                                         T* __restrict__ out, int64_t count,
+                                                         int accumulate) {
+  __shared__ T red[NT / 64];
+  const int64_t o = blockIdx.x;
+  const T* p = in + o * count;
+  T acc = T(0);
+  for (int64_t i = threadIdx.x; i < count; i += NT) acc += p[i];
+  for (int d = 32; d > 0; d >>= 1) acc += __shfl_xor(acc, d);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    T t = T(0);
+    for (int w = 0; w < NT / 64; ++w) t += red[w];
+    out[o] = accumulate ? out[o] + t : t;
+  }
+}
+
 // ------------------------------------------------------------------ host helpers
 int fill_stage(Stage& st, const void* x, const void* taps, int64_t n_in, int64_t n_out,
                int64_t x_off, int32_t n_scales, int32_t half, const int32_t* support,
@@ -730,6 +768,7 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   const int64_t span = TT + 2 * (int64_t)dil * half;
   const size_t lds = (size_t)(((span + 3) & ~3) + TT * channels) * cs;
   const int64_t blocks = rows * tiles;
+  if (n_el > INT32_MAX) return FDWT_ERR_ARG;
   int rc;
 #define BWH(TYPE, CPLX)                                                                       \
   do {                                                                                        \
@@ -738,8 +777,8 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
     rc = launch(k, blocks, lds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,      \
                 tiles);                                                                       \
     if (rc) return rc;                                                                        \
-    return launch(reduce_strided_kernel<TYPE>, cdiv(n_el, NT), 0, hs, (const TYPE*)workspace, \
-                  (TYPE*)gh, n_el, blocks, n_el, (int64_t)1, (int)accumulate);                \
+    return launch(reduce_cols_kernel<TYPE>, n_el, 0, hs, (const TYPE*)workspace, (TYPE*)gh,   \
+                  blocks, (int)accumulate);                                                   \
   } while (0)
   if (dtype == FDWT_F32) {
     if (channels == 2) BWH(float, true);
@@ -810,8 +849,8 @@ extern "C" int fdwt_mix_backward(const void* x, const void* taps, const void* a,
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
   const size_t lds = tile_lds(st, cs, 16);
-  // gab receives the per-(row, tile) partial sums (blocks, n_scales, 2); the caller reduces
-  // rows sharing a weight row d with fdwt_reduce_rows (deterministic order)
+  // the workspace receives per-(row, tile) partial sums (rows, tiles, n_scales, 2); the
+  // caller reduces the rows that share a weight row d in a fixed order
 #define MIXB(TYPE, CPLX)                                                                      \
   do {                                                                                        \
     auto k = mix_kernel<TYPE, CPLX, true>;                                                    \
