@@ -29,8 +29,9 @@ constexpr int VA = 2;            // consecutive analysis outputs per thread
 constexpr int GA = 2;            // thread groups per analysis chunk
 constexpr int CO = NT * VA * GA; // outputs per analysis chunk (2048)
 constexpr int VS = 2;            // consecutive synthesis pairs (u values) per thread
-constexpr int GS = 4;            // thread groups per synthesis pass
+constexpr int GS = 5;            // thread groups per synthesis pass
 constexpr int PS = NT * VS * GS; // coefficient pairs per synthesis pass (4096)
+constexpr int QR = 16;           // queue registers per thread (queue <= QR * NT samples)
 constexpr int MAXL_T = 32;       // largest templated filter length
 constexpr int MAX_TAPS = 256;    // longest filter accepted (PyWavelets' longest is 102)
 
@@ -58,7 +59,140 @@ struct SChainArgs {
   int32_t levels, taps, mode, off;
   int32_t capA, capB, capE, capD;
   int32_t split;  // output positions per workgroup in split mode (levels == 1), 0 = row
+  // whole-row workgroups: first coefficient pair of each level's passes
+  int32_t ub0[FDWT_MAX_LEVELS];
+  // the "queue": the high bands of the first qlevels levels (each a single pass), loaded into
+  // QR register slots of NT coefficients at kernel start.  Slot k holds coefficients
+  // qs_u0[k] .. qs_u0[k] + NT - 1 of the band qs_ptr[k] (rows of qs_nc[k] coefficients);
+  // level l < qlevels uses slots qs0[l] .. qs0[l] + qsn[l] - 1, of which its pass reads the
+  // first qlen[l] coefficients
+  const void* qs_ptr[QR];
+  int32_t qs_nc[QR];
+  int32_t qs_u0[QR];
+  int32_t qs0[FDWT_MAX_LEVELS];
+  int32_t qsn[FDWT_MAX_LEVELS];
+  int32_t qlen[FDWT_MAX_LEVELS];
+  int32_t qslots;
+  int32_t qlevels;
 };
+
+// Arguments of the whole-row synthesis chain (one workgroup per row).  The "queue" holds the
+// high bands of the first qlevels levels (each a single pass): at kernel start, queue slot k
+// loads coefficients qs_u0[k] .. qs_u0[k] + NT - 1 of band qs_ptr[k] (rows of qs_nc[k]) into
+// registers and then stages the first qs_len[k] of them at D[qs_pos[k] ..]; level l < qlevels
+// finds its band at D[qoff[l] + u - ub0].  Later levels stream their high band pass by pass.
+struct RChainArgs {
+  const void* approx;
+  const void* details[FDWT_MAX_LEVELS];
+  void* out;
+  const void* h0;
+  const void* h1;
+  int32_t nc[FDWT_MAX_LEVELS];
+  int32_t n_out[FDWT_MAX_LEVELS];
+  int32_t qoff[FDWT_MAX_LEVELS];
+  int32_t levels, taps, mode, off;
+  int32_t capA, capB, capD;
+  int32_t qslots, qlevels;
+  const void* qs_ptr[QR];
+  int32_t qs_nc[QR];
+  int32_t qs_u0[QR];
+  int32_t qs_pos[QR];
+  int32_t qs_len[QR];
+};
+
+// Geometry of one synthesis level (shared by the host and the kernel).  Outputs positions
+// [0, m) from nc coefficient pairs; positions outside [0, m) fold back onto "band" positions
+// near the ends (none in zero mode).  The passes run over coefficient pairs ub0, ub0 + PS, ..
+// and cover the positions [pbeg, pend).
+struct LevelGeom {
+  int md, P, pmin, pmax, band, nb, small, mw, plo, phi, pbeg, pend, ub0, npass;
+};
+
+__host__ __device__ inline LevelGeom level_geom(int nc, int m, int ncn, bool last, int L,
+                                                int off, int mode) {
+  LevelGeom g;
+  g.md = normalize_mode(mode, m);
+  g.P = mode_period(g.md, m);
+  g.pmin = off - (L - 1);
+  g.pmax = 2 * (nc - 1) + off;
+  const int nleft = g.md == FDWT_MODE_ZERO ? 0 : (g.pmin < 0 ? -g.pmin : 0);
+  const int nright = g.md == FDWT_MODE_ZERO ? 0 : (g.pmax - m + 1 > 0 ? g.pmax - m + 1 : 0);
+  const int nextra = nleft + nright;
+  g.band = nextra ? nextra + 2 : 0;
+  g.small = m <= 2 * g.band;
+  g.nb = nextra ? (g.small ? m : 2 * g.band) : 0;
+  g.mw = last ? m : (ncn < m ? ncn : m);  // positions the next level reads
+  g.plo = g.small ? m : g.band;           // positions written by the main pass: [plo, phi)
+  const int hi = m - g.band;
+  g.phi = g.small ? 0 : (hi < g.mw ? hi : g.mw);
+  g.pbeg = nextra ? (g.pmin < 0 ? g.pmin : 0) : 0;
+  g.pend = nextra ? (g.pmax + 1 > m ? g.pmax + 1 : m) : g.mw;
+  g.ub0 = ((g.pbeg + 1 - off) >> 1) & ~(VS - 1);
+  const int first = 2 * g.ub0 + off - 1;
+  g.npass = g.pend > first ? (g.pend - first + 2 * PS - 1) / (2 * PS) : 0;
+  return g;
+}
+
+// Per-level record of the whole-row synthesis kernel, kept in LDS (96 bytes).
+struct RLevel {
+  int32_t nc, m, mw, ncn;
+  int32_t ub0, npass, qoff, md;
+  int32_t P, pmin, pmax, band;
+  int32_t nb, plo, phi, pbeg;
+  int32_t pend, zend, small, pad;
+  const void* drow;
+  int32_t pad2[2];
+};
+constexpr int RLEVEL_BYTES = FDWT_MAX_LEVELS * (int)sizeof(RLevel);
+
+__device__ inline RLevel load_rlevel(const RLevel* p) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const v4i* q = reinterpret_cast<const v4i*>(p);
+  RLevel r;
+  int* w = reinterpret_cast<int*>(&r);
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const v4i t = q[k];
+    w[4 * k + 0] = __builtin_amdgcn_readfirstlane(t.x);
+    w[4 * k + 1] = __builtin_amdgcn_readfirstlane(t.y);
+    w[4 * k + 2] = __builtin_amdgcn_readfirstlane(t.z);
+    w[4 * k + 3] = __builtin_amdgcn_readfirstlane(t.w);
+  }
+  return r;
+}
+
+__host__ __device__ inline int floor_div(int a, int b) {  // b > 0
+  return a >= 0 ? a / b : -((-a + b - 1) / b);
+}
+
+// Per-level parameters of the synthesis chain as the kernel keeps them in LDS (64 bytes).
+struct LevelRec {
+  int32_t nc, n_out, ub0, qs0, qsn, qlen, ncn, pad;
+  const void* drow;  // this workgroup's row of the level's high band, or null
+  int32_t pad2[6];
+};
+constexpr int LREC_BYTES = FDWT_MAX_LEVELS * (int)sizeof(LevelRec);
+
+// Read one LevelRec (same address in every lane) and make its fields wave-uniform.
+__device__ inline LevelRec load_level(const LevelRec* p) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const v4i a = reinterpret_cast<const v4i*>(p)[0];
+  const v4i b = reinterpret_cast<const v4i*>(p)[1];
+  const v4i c = reinterpret_cast<const v4i*>(p)[2];
+  LevelRec r;
+  r.nc = __builtin_amdgcn_readfirstlane(a.x);
+  r.n_out = __builtin_amdgcn_readfirstlane(a.y);
+  r.ub0 = __builtin_amdgcn_readfirstlane(a.z);
+  r.qs0 = __builtin_amdgcn_readfirstlane(a.w);
+  r.qsn = __builtin_amdgcn_readfirstlane(b.x);
+  r.qlen = __builtin_amdgcn_readfirstlane(b.y);
+  r.ncn = __builtin_amdgcn_readfirstlane(b.z);
+  r.pad = 0;
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane(c.x);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane(c.y);
+  r.drow = reinterpret_cast<const void*>(lo | (hi << 32));
+  return r;
+}
 
 // ------------------------------------------------------------------ compute windows
 // Read W consecutive LDS elements starting at an address aligned to V elements with V-wide
@@ -346,29 +480,27 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
     }
     constexpr int SPAN_MAX = 2 * CO + (LT > 0 ? LT : MAXL_T) - 2;
     constexpr int PF = (SPAN_MAX + NT - 1) / NT;  // prefetch registers (template length)
-    T pf[PF];
+    // Prefetch registers hold raw samples: the loads are issued here, and the zero padding
+    // (a select) and the conversion happen when the chunk is staged, so no wait follows a
+    // load where it is issued.  Positions outside the row load the sample their extension
+    // maps to (row position 0 under zero padding).
+    S pf[PF] = {};
 
-    auto fetch = [&](int c, T (&r)[PF]) {
+    auto fetch = [&](int c, S (&r)[PF]) {
       const int p0 = 2 * c * CO + pmin;
       const bool interior = p0 >= 0 && p0 + SPAN_MAX <= n;
 #pragma unroll
       for (int k = 0; k < PF; ++k) {
         const int idx = tid + k * NT;
-        const int p = p0 + idx;
-        T v = T(0);
+        int i = p0 + idx;
         if (idx < SPAN_MAX) {
-          if (interior) {
-            v = T(Storage<S>::load(xrow, p));
-          } else {
-            // unconditional load of a valid index, zeroed by select (zero padding)
+          if (!interior && (i < 0 || i >= n)) {
             bool valid = true;
-            int i = p;
-            if (p < 0 || p >= n) i = ext_index(p, n, mode0, P, valid);
-            const T w = T(Storage<S>::load(xrow, valid ? i : 0));
-            v = valid ? w : T(0);
+            i = ext_index(i, n, mode0, P, valid);
+            if (!valid) i = 0;
           }
+          r[k] = xrow[i];
         }
-        r[k] = v;
       }
     };
 
@@ -376,10 +508,14 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
       if (c_begin < c_end) fetch(c_begin, pf);
       for (int c = c_begin; c < c_end; ++c) {
         __syncthreads();
+        const int p0 = 2 * c * CO + pmin;
 #pragma unroll
         for (int k = 0; k < PF; ++k) {
           const int idx = tid + k * NT;
-          if (idx < SPAN_MAX) B[idx] = pf[k];
+          const int p = p0 + idx;
+          if (idx < SPAN_MAX)
+            B[idx] = (mode0 == FDWT_MODE_ZERO && (p < 0 || p >= n)) ? T(0)
+                                                                  : T(Storage<S>::load(pf + k, 0));
         }
         __syncthreads();
         if (c + 1 < c_end) fetch(c + 1, pf);
@@ -465,7 +601,10 @@ template <typename S, typename T, int LT>
 __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, int64_t rows,
                                                              int wg_per_row) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* const A = reinterpret_cast<T*>(smem_raw);
+  // per-level parameters, copied from the arguments into LDS once: the level loop reads them
+  // with one wave-uniform LDS access instead of a chain of scalar loads at dynamic offsets
+  LevelRec* const lrec = reinterpret_cast<LevelRec*>(smem_raw);
+  T* const A = reinterpret_cast<T*>(smem_raw + LREC_BYTES);
   T* const B = A + args.capA;
   T* const E = B + args.capB;
   int* const ET = reinterpret_cast<int*>(E + args.capE);
@@ -501,63 +640,95 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
     h1 = tap_lds + L;
   }
 
+  // first coefficient pair of a level's passes (aligned to VS): precomputed by the host for
+  // whole-row workgroups; split workgroups start at their own window
+  auto level_first_pass = [&](int lv) {
+    if (!args.split) return args.ub0[lv];
+    return ((part * args.split + 1 - off) >> 1) & ~(VS - 1);
+  };
+  auto drow_of = [&](int lv) -> const S* {
+    return args.details[lv] ? static_cast<const S*>(args.details[lv]) + row * (int64_t)args.nc[lv]
+                            : nullptr;
+  };
+  if (tid < args.levels) {
+    LevelRec r;
+    r.nc = args.nc[tid];
+    r.n_out = args.n_out[tid];
+    r.ub0 = level_first_pass(tid);
+    r.qs0 = args.qs0[tid];
+    r.qsn = args.qsn[tid];
+    r.qlen = args.qlen[tid];
+    r.ncn = tid + 1 < args.levels ? args.nc[tid + 1] : 0;
+    r.pad = 0;
+    r.drow = drow_of(tid);
+    lrec[tid] = r;
+  }
+  const int dspan = PS + H + 4;
+  constexpr int PFD = PS / NT + 1;  // dspan <= PFD * NT since H + 4 <= NT
+  // Prefetch registers hold raw coefficients: the loads are issued here and range-masked and
+  // converted only when the pass is staged, so no wait follows a load where it is issued.
+  // (The load index is clamped into the row; positions outside it are zeroed at staging.)
+  S pf[PFD] = {};
+  auto fetch_d = [&](const S* dr, int ncl, int pbl) {
+    if (!dr) return;
+#pragma unroll
+    for (int k = 0; k < PFD; ++k) {
+      // blocks of NT entirely outside the coefficients are skipped (block-uniform test)
+      if (k * NT < dspan && pbl + k * NT < ncl && pbl + k * NT + NT > 0)
+        pf[k] = dr[min(max(pbl + tid + k * NT, 0), ncl - 1)];
+    }
+  };
+  // every HBM read the kernel needs for its small levels is issued here, before the low band
+  // is staged: the queue (levels 0 .. qlevels - 1) and the first pass of the next level
+  S pq[QR] = {};
+#pragma unroll
+  for (int k = 0; k < QR; ++k) {
+    if (k < args.qslots && args.qs_ptr[k]) {
+      const int ncl = args.qs_nc[k];
+      const S* dr = static_cast<const S*>(args.qs_ptr[k]) + row * (int64_t)ncl;
+      pq[k] = dr[min(max(args.qs_u0[k] + tid, 0), ncl - 1)];
+    }
+  }
+  if (args.qlevels < args.levels) {
+    const int fl = args.qlevels;
+    fetch_d(drow_of(fl), args.nc[fl], level_first_pass(fl));
+  }
+
   // stage the coarsest low band (or, in split mode, this workgroup's window of it)
   int u_lo = 0;
   {
     const int nc = args.nc[0];
     const S* ag = args.approx ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
     if (args.split) u_lo = ((((part * args.split) - off) >> 1) - 4) & ~3;
-    for (int k = tid; k < args.capA; k += NT) {
-      const int u = u_lo + k - ZL;
-      T v = T(0);
+    // whole rows stage the band and the margin that level 0 reads (coefficients up to
+    // nc + L + 2 VS + 16); the loads are issued AB at a time so that their latencies overlap
+    constexpr int AB = 9;
+    const int kend = args.split ? args.capA : min(args.capA, ZL + nc + L + 2 * VS + 16);
+    // (raw loads at clamped indices first, range masks and conversions after all of them)
+    for (int k0 = tid; k0 < kend; k0 += AB * NT) {
+      S v[AB] = {};
       if (ag) {
-        const T w = T(Storage<S>::load(ag, min(max(u, 0), nc - 1)));
-        v = (u >= 0 && u < nc) ? w : T(0);
+#pragma unroll
+        for (int j = 0; j < AB; ++j) v[j] = ag[min(max(u_lo + k0 + j * NT - ZL, 0), nc - 1)];
       }
-      A[k] = v;
+#pragma unroll
+      for (int j = 0; j < AB; ++j) {
+        const int k = k0 + j * NT;
+        const int u = u_lo + k - ZL;
+        if (k < kend) A[k] = (ag && u >= 0 && u < nc) ? T(Storage<S>::load(v + j, 0)) : T(0);
+      }
     }
   }
   __syncthreads();
 
-  // first coefficient pair of a level's passes (aligned to VS); whole-row workgroups of
-  // non-zero modes start at the extended range [pmin, ...) (see below)
-  auto level_first_pass = [&](int lv) {
-    const int ncl = args.nc[lv];
-    const int ml = args.n_out[lv];
-    const int mdl = normalize_mode(mode, ml);
-    const int pminl = off - (L - 1);
-    const int pmaxl = 2 * (ncl - 1) + off;
-    const int nx = mdl == FDWT_MODE_ZERO ? 0 : max(0, -pminl) + max(0, pmaxl - ml + 1);
-    const int ib = args.split ? part * args.split : 0;
-    const int pbeg = (nx > 0 && !args.split) ? min(0, pminl) : ib;
-    return ((pbeg + 1 - off) >> 1) & ~(VS - 1);
-  };
-  const int dspan = PS + H + 4;
-  constexpr int PFD = PS / NT + 1;  // dspan <= PFD * NT since H + 4 <= NT
-  T pf[PFD];
-  auto fetch_d = [&](const S* dr, int ncl, int pbl) {
-#pragma unroll
-    for (int k = 0; k < PFD; ++k) {
-      const int idx = tid + k * NT;
-      const int u = pbl + idx;
-      T v = T(0);
-      // blocks of NT entirely outside the coefficients are skipped (block-uniform test)
-      if (dr && idx < dspan && pbl + k * NT < ncl && pbl + k * NT + NT > 0) {
-        const T w = T(Storage<S>::load(dr, min(max(u, 0), ncl - 1)));
-        v = (u >= 0 && u < ncl) ? w : T(0);
-      }
-      pf[k] = v;
-    }
-  };
-
   T* src = A;
   T* dst = B;
   for (int l = 0; l < args.levels; ++l) {
-    const int nc = args.nc[l];
-    const int m = args.n_out[l];
+    const LevelRec lr = load_level(lrec + l);
+    const int nc = lr.nc;
+    const int m = lr.n_out;
     const bool last = l + 1 == args.levels;
-    const S* drow = args.details[l] ? static_cast<const S*>(args.details[l]) + row * (int64_t)nc
-                                    : nullptr;
+    const S* drow = static_cast<const S*>(lr.drow);
     const T* a0 = src + ZL - u_lo;  // a0[u] = low band coefficient u
     const int md = normalize_mode(mode, m);
     const int P = mode_period(md, m);
@@ -585,9 +756,9 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
     }
     const int p_begin = inpass ? min(0, pmin) : i_begin;
     const int p_end = inpass ? max(m, pmax + 1) : i_end;
-    const int ub0 = level_first_pass(l);
+    const int ub0 = lr.ub0;
     int pb = ub0;
-    if (l == 0 && 2 * pb + off - 1 < p_end) fetch_d(drow, nc, pb);  // later levels: prefetched
+    const bool from_queue = l < args.qlevels;  // this level's d is in the queue
 
     for (int k = tid; k < nextra; k += NT) {
       const int p = k < nleft ? pmin + k : m + (k - nleft);
@@ -615,21 +786,37 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
     const int plain_hi = min(i_end, m - band);
     for (; 2 * pb + off - 1 < p_end; pb += PS) {
       __syncthreads();  // previous pass done with D (F / E / ET written)
+      if (from_queue) {
+        // a queued level has a single pass, held by queue slots s0 .. s0 + sn - 1
+        const int s0 = lr.qs0, sn = lr.qsn, len = lr.qlen;
 #pragma unroll
-      for (int k = 0; k < PFD; ++k) {
-        const int idx = tid + k * NT;
-        if (idx < dspan) D[idx] = pf[k];
+        for (int k = 0; k < QR; ++k) {
+          if (k >= s0 && k < s0 + sn) {
+            const int idx = (k - s0) * NT + tid;
+            const int u = pb + idx;
+            if (idx < len)
+              D[idx] = (drow && u >= 0 && u < nc) ? T(Storage<S>::load(pq + k, 0)) : T(0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < PFD; ++k) {
+          const int idx = tid + k * NT;
+          const int u = pb + idx;
+          if (idx < dspan)
+            D[idx] = (drow && u >= 0 && u < nc) ? T(Storage<S>::load(pf + k, 0)) : T(0);
+        }
       }
       __syncthreads();
       const int pn = pb + PS;
-      if (2 * pn + off - 1 < p_end) {
-        fetch_d(drow, nc, pn);
-      } else if (!last) {
-        // last pass of this level: request the first pass of the next level now
-        const int nl = l + 1;
-        fetch_d(args.details[nl] ? static_cast<const S*>(args.details[nl]) + row * (int64_t)args.nc[nl]
-                                 : nullptr,
-                args.nc[nl], level_first_pass(nl));
+      if (!from_queue) {
+        if (2 * pn + off - 1 < p_end) {
+          fetch_d(drow, nc, pn);
+        } else if (!last) {
+          // last pass of this level: request the first pass of the next level now
+          const LevelRec nr = load_level(lrec + l + 1);
+          fetch_d(static_cast<const S*>(nr.drow), nr.nc, nr.ub0);
+        }
       }
 #pragma unroll
       for (int g = 0; g < GS; ++g) {
@@ -656,6 +843,7 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
           }
           continue;
         }
+        // positions near the row ends (fold band, out-of-range values, partial rows)
 #pragma unroll
         for (int j = 0; j < 2 * VS; ++j) {
           const int i = i0 + j;
@@ -690,15 +878,341 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
     __syncthreads();
     if (!last) {
       // zero margins of the next low band (which is the first nc[l+1] outputs)
-      const int ncn = args.nc[l + 1];
+      // (the next level reads coefficients -ZL .. ncn + L + 2 VS + 8 at most)
+      const int ncn = lr.ncn;
       const int cap_dst = (l % 2 == 0) ? args.capB : args.capA;  // dst is B after even levels
+      const int zend = min(cap_dst, ZL + ncn + L + 2 * VS + 16);
       for (int k = tid; k < ZL; k += NT) dst[k] = T(0);
-      for (int k = ZL + ncn + tid; k < cap_dst; k += NT) dst[k] = T(0);
+      for (int k = ZL + ncn + tid; k < zend; k += NT) dst[k] = T(0);
       __syncthreads();
       T* t = src;
       src = dst;
       dst = t;
     }
+  }
+}
+
+// Value z(p) of one synthesis position from LDS: the low band a0[u] (zero margins) and the
+// high band dp[u] (this pass's window), z(p) = sum_t h0[2t+par] a[u+t] + h1[2t+par] d[u+t].
+template <typename T, int LT>
+__device__ inline T synthesis_lds_point(const T* a0, const T* dp, int p, int off, const T* h0,
+                                        const T* h1, int L) {
+  const int r = p - off;
+  const int par = r & 1;
+  const int u = (r + par) >> 1;
+  T z = T(0);
+  if constexpr (LT > 0) {
+    // both parities with constant tap indices (a tap chosen by the lane's parity would need
+    // the register-held taps indexed at run time), then the lane's parity selects
+    T ze = T(0), zo = T(0);
+#pragma unroll
+    for (int t = 0; t < LT / 2; ++t) {
+      const T av = a0[u + t];
+      const T dv = dp[u + t];
+      ze = fma(h0[2 * t], av, ze);
+      ze = fma(h1[2 * t], dv, ze);
+      zo = fma(h0[2 * t + 1], av, zo);
+      zo = fma(h1[2 * t + 1], dv, zo);
+    }
+    z = par ? zo : ze;
+  } else {
+    for (int t = 0; t < L / 2; ++t) {
+      z = fma(h0[2 * t + par], a0[u + t], z);
+      z = fma(h1[2 * t + par], dp[u + t], z);
+    }
+  }
+  return z;
+}
+
+// Sum of z over the extended positions in [lo, hi) that fold onto row position i (i itself
+// when it lies in [lo, hi)): the positions congruent modulo the period P to i and, for the
+// mirroring extensions, to the mirror image of i.
+template <typename T, int LT>
+__device__ inline T band_sum(int i, int lo, int hi, int m, int md, int P, int pmin, int pmax,
+                             const T* a0, const T* dp, int off, const T* h0, const T* h1,
+                             int L) {
+  T s = T(0);
+  if (i >= lo && i < hi) s += synthesis_lds_point<T, LT>(a0, dp, i, off, h0, h1, L);
+  int mirror = -1;
+  if (md == FDWT_MODE_SYMMETRIC) mirror = P - 1 - i;
+  else if (md == FDWT_MODE_REFLECT && i > 0 && i < m - 1) mirror = P - i;
+  else if (md == FDWT_MODE_PERIODIZATION && i == m - 1 && P > m) mirror = m;
+  const int a = lo > pmin ? lo : pmin;
+  const int b = hi < pmax + 1 ? hi : pmax + 1;
+  for (int w = 0; w < 2; ++w) {
+    const int base = w == 0 ? i : mirror;
+    if (base < 0) continue;
+    for (int k = floor_div(a - base + P - 1, P); base + k * P < b; ++k) {
+      const int p = base + k * P;
+      if (p < 0 || p >= m) s += synthesis_lds_point<T, LT>(a0, dp, p, off, h0, h1, L);
+    }
+  }
+  return s;
+}
+
+// Whole-row synthesis chain: one workgroup reconstructs one row through all levels.  The
+// low band lives in LDS (A <-> B ping-pong with zero margins), the high bands are staged in D
+// (the queued small levels once at kernel start, the others pass by pass from prefetch
+// registers).  Each level writes its interior positions from the main pass and the positions
+// near the row ends from "band lanes" (the highest thread ids), which add up every extended
+// position that folds onto them; a level therefore needs no extra fold pass.
+template <typename S, typename T, int LT>
+__global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  RLevel* const lrec = reinterpret_cast<RLevel*>(smem_raw);
+  T* const A = reinterpret_cast<T*>(smem_raw + RLEVEL_BYTES);
+  T* const B = A + args.capA;
+  T* const D = B + args.capB;
+  T* const tap_lds = D + args.capD;
+
+  const int64_t row = blockIdx.x;
+  const int L = LT > 0 ? LT : args.taps;
+  const int H = L / 2;
+  const int ZL = (L + 3) & ~3;
+  const int off = args.off;
+  const int mode = args.mode;
+  const int levels = args.levels;
+  const int tid = threadIdx.x;
+
+  const T* gh0 = static_cast<const T*>(args.h0);
+  const T* gh1 = static_cast<const T*>(args.h1);
+  T h0r[LT > 0 ? LT : 1], h1r[LT > 0 ? LT : 1];
+  const T* h0;
+  const T* h1;
+  if constexpr (LT > 0) {
+#pragma unroll
+    for (int i = 0; i < LT; ++i) {
+      h0r[i] = gh0[i];
+      h1r[i] = gh1[i];
+    }
+    h0 = h0r;
+    h1 = h1r;
+  } else {
+    load_taps(gh0, gh1, tap_lds, tap_lds + L, L, false);
+    h0 = tap_lds;
+    h1 = tap_lds + L;
+  }
+
+  // level table (one lane per level)
+  if (tid < levels) {
+    const int l = tid;
+    const bool last = l + 1 == levels;
+    RLevel r;
+    r.nc = args.nc[l];
+    r.m = args.n_out[l];
+    r.ncn = last ? 0 : args.nc[l + 1];
+    const LevelGeom g = level_geom(r.nc, r.m, r.ncn, last, L, off, mode);
+    r.mw = g.mw;
+    r.ub0 = g.ub0;
+    r.npass = g.npass;
+    r.qoff = args.qoff[l];
+    r.md = g.md;
+    r.P = g.P;
+    r.pmin = g.pmin;
+    r.pmax = g.pmax;
+    r.band = g.band;
+    r.nb = g.nb;
+    r.plo = g.plo;
+    r.phi = g.phi;
+    r.pbeg = g.pbeg;
+    r.pend = g.pend;
+    const int cap_dst = (l % 2 == 0) ? args.capB : args.capA;  // level l writes B if l even
+    const int zend = ZL + r.ncn + L + 2 * VS + 16;
+    r.zend = last ? 0 : (zend < cap_dst ? zend : cap_dst);
+    r.small = g.small;
+    r.pad = 0;
+    r.drow = args.details[l]
+                 ? static_cast<const S*>(args.details[l]) + row * (int64_t)r.nc
+                 : nullptr;
+    r.pad2[0] = r.pad2[1] = 0;
+    lrec[l] = r;
+  }
+
+  // Prefetch registers hold raw coefficients; the loads are issued here and range-masked and
+  // converted only when staged, so no wait follows a load where it is issued.
+  const int dspan = PS + H + 4;
+  constexpr int PFD = PS / NT + 1;  // dspan <= PFD * NT since H + 4 <= NT
+  S pf[PFD] = {};
+  auto fetch_d = [&](const S* dr, int ncl, int pbl) {
+    if (!dr) return;
+#pragma unroll
+    for (int k = 0; k < PFD; ++k) {
+      // blocks of NT entirely outside the coefficients are skipped (block-uniform test)
+      if (k * NT < dspan && pbl + k * NT < ncl && pbl + k * NT + NT > 0)
+        pf[k] = dr[min(max(pbl + tid + k * NT, 0), ncl - 1)];
+    }
+  };
+  S pq[QR] = {};
+#pragma unroll
+  for (int k = 0; k < QR; ++k) {
+    if (k < args.qslots && args.qs_ptr[k]) {
+      const int ncl = args.qs_nc[k];
+      const S* dr = static_cast<const S*>(args.qs_ptr[k]) + row * (int64_t)ncl;
+      pq[k] = dr[min(max(args.qs_u0[k] + tid, 0), ncl - 1)];
+    }
+  }
+  if (args.qlevels < levels) {
+    const int fl = args.qlevels;
+    const bool flast = fl + 1 == levels;
+    const int ncl = args.nc[fl];
+    const LevelGeom g =
+        level_geom(ncl, args.n_out[fl], flast ? 0 : args.nc[fl + 1], flast, L, off, mode);
+    const S* dr = args.details[fl] ? static_cast<const S*>(args.details[fl]) + row * (int64_t)ncl
+                                   : nullptr;
+    fetch_d(dr, ncl, g.ub0);
+  }
+
+  // the coarsest low band -> A, with zero margins; loads issued AB at a time
+  {
+    const int nc = args.nc[0];
+    const S* ag = args.approx ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
+    constexpr int AB = 9;
+    const int kend = min(args.capA, ZL + nc + L + 2 * VS + 16);
+    for (int k0 = tid; k0 < kend; k0 += AB * NT) {
+      S v[AB] = {};
+      if (ag) {
+#pragma unroll
+        for (int j = 0; j < AB; ++j) v[j] = ag[min(max(k0 + j * NT - ZL, 0), nc - 1)];
+      }
+#pragma unroll
+      for (int j = 0; j < AB; ++j) {
+        const int k = k0 + j * NT;
+        const int u = k - ZL;
+        if (k < kend) A[k] = (ag && u >= 0 && u < nc) ? T(Storage<S>::load(v + j, 0)) : T(0);
+      }
+    }
+  }
+  // the queued high bands -> D
+#pragma unroll
+  for (int k = 0; k < QR; ++k) {
+    if (k < args.qslots && tid < args.qs_len[k]) {
+      const int u = args.qs_u0[k] + tid;
+      const bool ok = args.qs_ptr[k] && u >= 0 && u < args.qs_nc[k];
+      D[args.qs_pos[k] + tid] = ok ? T(Storage<S>::load(pq + k, 0)) : T(0);
+    }
+  }
+  __syncthreads();
+
+  T* src = A;
+  T* dst = B;
+  constexpr int BK = 3;  // band positions per band lane (at most 3 NT per level)
+  for (int l = 0; l < levels; ++l) {
+    const RLevel lr = load_rlevel(lrec + l);
+    const bool last = l + 1 == levels;
+    const int m = lr.m;
+    const int nc = lr.nc;
+    const T* a0 = src + ZL;  // a0[u] = low band coefficient u
+    S* orow = last ? static_cast<S*>(args.out) + row * (int64_t)m : nullptr;
+    const S* drow = static_cast<const S*>(lr.drow);
+
+    // zero the margins of the next low band (dst holds positions [0, mw) afterwards)
+    if (!last) {
+      for (int k = tid; k < ZL; k += NT) dst[k] = T(0);
+      for (int k = ZL + lr.ncn + tid; k < lr.zend; k += NT) dst[k] = T(0);
+    }
+
+    // 16-byte stores when provably aligned: off == 1 puts every thread's first position on a
+    // multiple of 4, and m % 4 == 0 keeps rows 16-byte aligned in global memory
+    const bool vec_out = std::is_same<S, float>::value && off == 1 && (m % 4) == 0;
+    const bool vec_lds = off == 1;
+    T acc[BK];
+#pragma unroll
+    for (int j = 0; j < BK; ++j) acc[j] = T(0);
+    const int bt = NT - 1 - tid;  // band lane index
+
+    for (int pi = 0; pi < lr.npass; ++pi) {
+      const int pb = lr.ub0 + pi * PS;
+      const T* dp;  // dp[u] = high band coefficient u (this pass's window)
+      if (lr.qoff >= 0) {
+        dp = D + lr.qoff - lr.ub0;
+      } else {
+        if (pi > 0) __syncthreads();  // the previous pass is done with D
+#pragma unroll
+        for (int k = 0; k < PFD; ++k) {
+          const int idx = tid + k * NT;
+          const int u = pb + idx;
+          if (idx < dspan)
+            D[idx] = (drow && u >= 0 && u < nc) ? T(Storage<S>::load(pf + k, 0)) : T(0);
+        }
+        __syncthreads();
+        if (pi + 1 < lr.npass) {
+          fetch_d(drow, nc, pb + PS);
+        } else if (!last) {
+          const RLevel nr = load_rlevel(lrec + l + 1);
+          if (nr.qoff < 0) fetch_d(static_cast<const S*>(nr.drow), nr.nc, nr.ub0);
+        }
+        dp = D - pb;
+      }
+
+      // main pass: positions [plo, phi)
+#pragma unroll
+      for (int g = 0; g < GS; ++g) {
+        const int lu = (g * NT + tid) * VS;  // coefficient offset inside the pass
+        const int ub = pb + lu;
+        const int i0 = 2 * ub + off - 1;     // first of this thread's 2 * VS positions
+        if (i0 + 2 * VS <= lr.plo || i0 >= lr.phi) continue;
+        T zo[VS], ze[VS];
+        synthesis_block<T, LT>(a0 + ub, dp + ub, h0, h1, L, zo, ze);
+        T v[2 * VS];
+#pragma unroll
+        for (int q = 0; q < VS; ++q) {
+          v[2 * q] = zo[q];
+          v[2 * q + 1] = ze[q];
+        }
+        if (VS == 2 && i0 >= lr.plo && i0 + 2 * VS <= lr.phi && (last ? vec_out : vec_lds)) {
+          typedef T v4 __attribute__((ext_vector_type(4)));
+          const v4 w = {v[0], v[1], v[2], v[3]};
+          if (last) {
+            if constexpr (std::is_same<S, float>::value)
+              *reinterpret_cast<v4*>(orow + i0) = w;
+          } else {
+            *reinterpret_cast<v4*>(dst + ZL + i0) = w;
+          }
+          continue;
+        }
+#pragma unroll
+        for (int j = 0; j < 2 * VS; ++j) {
+          const int i = i0 + j;
+          if (i >= lr.plo && i < lr.phi) {
+            if (last) Storage<S>::store(orow, i, v[j]);
+            else dst[ZL + i] = v[j];
+          }
+        }
+      }
+
+      // band lanes: the positions of this pass that fold onto band positions
+      if (bt < lr.nb) {
+        const int q0 = 2 * pb + off - 1;
+        const int lo = max(q0, lr.pbeg);
+        const int hi = min(q0 + 2 * PS, lr.pend);
+#pragma unroll
+        for (int j = 0; j < BK; ++j) {
+          const int b = bt + j * NT;
+          if (b < lr.nb) {
+            const int i = (lr.small || b < lr.band) ? b : m - 2 * lr.band + b;
+            acc[j] += band_sum<T, LT>(i, lo, hi, m, lr.md, lr.P, lr.pmin, lr.pmax, a0, dp, off,
+                                      h0, h1, L);
+          }
+        }
+      }
+    }
+    if (bt < lr.nb) {
+#pragma unroll
+      for (int j = 0; j < BK; ++j) {
+        const int b = bt + j * NT;
+        if (b < lr.nb) {
+          const int i = (lr.small || b < lr.band) ? b : m - 2 * lr.band + b;
+          if (i < lr.mw) {
+            if (last) Storage<S>::store(orow, i, acc[j]);
+            else dst[ZL + i] = acc[j];
+          }
+        }
+      }
+    }
+    __syncthreads();
+    T* t = src;
+    src = dst;
+    dst = t;
   }
 }
 
@@ -741,6 +1255,16 @@ int launch_schain(const SChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
   return 0;
 }
 
+template <typename S, typename T, int LT>
+int launch_rchain(const RChainArgs& a, int64_t rows, size_t lds, hipStream_t st) {
+  auto k = synthesis_rows_kernel<S, T, LT>;
+  static const bool lds_ok = allow_full_lds(k);
+  (void)lds_ok;
+  hipLaunchKernelGGL(k, dim3((unsigned)rows), dim3(NT), lds, st, a);
+  FDWT_CHECK_LAUNCH();
+  return 0;
+}
+
 #define FDWT_TAPS_SWITCH(L, FN, ...)                                                     \
   switch (L) {                                                                           \
     case 2: return FN<S, float, 2>(__VA_ARGS__);                                         \
@@ -774,6 +1298,23 @@ int run_schain(const SChainArgs& a, int64_t rows, int wg, size_t lds, hipStream_
                bool templated) {
   if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_schain, a, rows, wg, lds, st) }
   return launch_schain<S, float, 0>(a, rows, wg, lds, st);
+}
+
+template <typename S>
+int run_rchain(const RChainArgs& a, int64_t rows, size_t lds, hipStream_t st, bool templated) {
+  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_rchain, a, rows, lds, st) }
+  return launch_rchain<S, float, 0>(a, rows, lds, st);
+}
+
+int dispatch_rchain(const RChainArgs& a, int64_t rows, size_t lds, int dtype, hipStream_t st) {
+  const bool templ = a.taps <= MAXL_T;
+  switch (dtype) {
+    case FDWT_F32: return run_rchain<float>(a, rows, lds, st, templ);
+    case FDWT_F16: return run_rchain<__half>(a, rows, lds, st, templ);
+    case FDWT_BF16: return run_rchain<bf16_t>(a, rows, lds, st, templ);
+    case FDWT_F64: return launch_rchain<double, double, 0>(a, rows, lds, st);
+    default: return FDWT_ERR_ARG;
+  }
 }
 
 int dispatch_achain(const AChainArgs& a, int64_t rows, int wg, size_t lds, int dtype,
@@ -856,7 +1397,8 @@ using namespace fdwt;
 
 extern "C" int64_t fdwt_chain_max_length(int32_t taps, int32_t dtype) {
   // analysis: A ~ n/2 + 2L, B ~ max(stage, n/4 + 2L); synthesis: similar.  Keep <= 160 KiB.
-  const int64_t budget = 160 * 1024 / compute_size(dtype) - 4 * (int64_t)taps - 4 * MAXL_T - 64;
+  const int64_t budget =
+      (160 * 1024 - LREC_BYTES) / compute_size(dtype) - 4 * (int64_t)taps - 4 * MAXL_T - 64;
   const int64_t stage = 2 * (int64_t)CO + MAXL_T;
   // n/2 + max(stage, n/4) + 6L <= budget
   int64_t n = 2 * (budget - stage - 6 * (int64_t)taps);
@@ -918,6 +1460,72 @@ extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* ap
   return dispatch_achain(a, rows, wg, lds, dtype, static_cast<hipStream_t>(stream));
 }
 
+// Whole-row synthesis chain: LDS layout, queue placement and launch.
+int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st) {
+  RChainArgs a{};
+  const int levels = s.levels, L = s.taps, off = s.off, mode = s.mode;
+  a.approx = s.approx;
+  a.out = s.out;
+  a.h0 = s.h0;
+  a.h1 = s.h1;
+  a.levels = levels;
+  a.taps = L;
+  a.mode = mode;
+  a.off = off;
+  const int64_t zl = (L + 3) & ~3;
+  const int64_t margin = zl + L + 2 * VS + 24;
+  int64_t capA = s.nc[0] + margin, capB = 4;
+  const int64_t capD = (PS + L / 2 + 8 + 3) & ~3;
+  int slot = 0;
+  int64_t qpos = 0;
+  bool queue_open = true;
+  for (int l = 0; l < levels; ++l) {
+    const bool last = l + 1 == levels;
+    a.details[l] = s.details[l];
+    a.nc[l] = s.nc[l];
+    a.n_out[l] = s.n_out[l];
+    a.qoff[l] = -1;
+    const LevelGeom g = level_geom(s.nc[l], s.n_out[l], last ? 0 : s.nc[l + 1], last, L, off, mode);
+    if (g.nb > 3 * NT) return FDWT_ERR_TOO_LONG;
+    if (!last) {
+      const int64_t need = s.n_out[l] + margin;  // output of level l = low band of level l + 1
+      if (l % 2 == 0) capB = std::max(capB, need);
+      else capA = std::max(capA, need);
+    }
+    // the queue takes a prefix of the levels (never the last), each a single pass
+    if (queue_open && !last) {
+      const int64_t ub_last = (g.pend - off) >> 1;
+      const int64_t len = ub_last - g.ub0 + 2 * VS + L / 2 + 4;
+      const int ns = (int)cdiv(len, NT);
+      if (g.npass != 1 || slot + ns > QR || qpos + len > capD) {
+        queue_open = false;
+      } else {
+        a.qoff[l] = (int32_t)qpos;
+        for (int k = 0; k < ns; ++k, ++slot) {
+          a.qs_ptr[slot] = s.details[l];
+          a.qs_nc[slot] = s.nc[l];
+          a.qs_u0[slot] = (int32_t)(g.ub0 + (int64_t)k * NT);
+          a.qs_pos[slot] = (int32_t)(qpos + (int64_t)k * NT);
+          a.qs_len[slot] = (int32_t)std::min<int64_t>(NT, len - (int64_t)k * NT);
+        }
+        qpos = (qpos + len + 3) & ~(int64_t)3;
+        a.qlevels = l + 1;
+      }
+    } else {
+      queue_open = false;
+    }
+  }
+  a.qslots = slot;
+  a.capA = (int)((capA + 3) & ~3);
+  a.capB = (int)((capB + 3) & ~3);
+  a.capD = (int)capD;
+  const size_t lds = (size_t)RLEVEL_BYTES +
+                     (size_t)(a.capA + a.capB + a.capD + 2 * L + 4) * compute_size(dtype);
+  if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
+  if (rows > INT32_MAX) return FDWT_ERR_ARG;
+  return dispatch_rchain(a, rows, lds, dtype, st);
+}
+
 extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* details, void* out,
                                     const void* h0, const void* h1, int64_t rows,
                                     const int64_t* nc, const int64_t* n_out, int32_t levels,
@@ -958,6 +1566,45 @@ extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* detai
     a.split = (int)per;
     wg = (int)cdiv(m, per);
   }
+  if (!a.split) return synthesis_rows(a, rows, dtype, static_cast<hipStream_t>(stream));
+  // per-level pass geometry of whole-row workgroups, and the queue of small-level high bands
+  a.qslots = 0;
+  a.qlevels = 0;
+  if (!a.split) {
+    int slot = 0;
+    bool fits = true;
+    for (int l = 0; l < levels; ++l) {
+      const int md = normalize_mode(mode, (int)n_out[l]);
+      const int64_t pmin = off - (taps - 1);
+      const int64_t pmax = 2 * (nc[l] - 1) + off;
+      const int64_t nx = md == FDWT_MODE_ZERO ? 0
+                         : std::max<int64_t>(0, -pmin) + std::max<int64_t>(0, pmax - n_out[l] + 1);
+      const int64_t pbeg = nx > 0 ? std::min<int64_t>(0, pmin) : 0;
+      const int64_t pend = nx > 0 ? std::max<int64_t>(n_out[l], pmax + 1) : n_out[l];
+      const int64_t ub0 = ((pbeg + 1 - off) >> 1) & ~(int64_t)(VS - 1);
+      a.ub0[l] = (int32_t)ub0;
+      // the queue takes a prefix of the levels (never the last), each a single pass
+      if (fits && l + 1 < levels) {
+        const int64_t ub_last = (pend - off) >> 1;
+        const int64_t len = ub_last - ub0 + 2 * VS + taps / 2 + 4;
+        const int ns = (int)cdiv(len, NT);
+        if (ub_last - ub0 + 1 > PS || slot + ns > QR) {
+          fits = false;
+        } else {
+          a.qs0[l] = slot;
+          a.qsn[l] = ns;
+          a.qlen[l] = (int32_t)len;
+          for (int k = 0; k < ns; ++k, ++slot) {
+            a.qs_ptr[slot] = a.details[l];
+            a.qs_nc[slot] = (int32_t)nc[l];
+            a.qs_u0[slot] = (int32_t)(ub0 + (int64_t)k * NT);
+          }
+          a.qlevels = l + 1;
+        }
+      }
+    }
+    a.qslots = slot;
+  }
   int capA, capB, capE, capD;
   schain_caps(nc, n_out, levels, taps, off, mode, a.split, &capA, &capB, &capE, &capD);
   a.capA = capA;
@@ -966,7 +1613,8 @@ extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* detai
   a.capD = capD;
   const int cs = compute_size(dtype);
   // A, B, E, ET (ints), F, D, taps
-  const size_t lds = (size_t)(capA + capB + capE + (2 * capE + 8) + capD + 2 * taps + 4) * cs +
+  const size_t lds = (size_t)LREC_BYTES +
+                     (size_t)(capA + capB + capE + (2 * capE + 8) + capD + 2 * taps + 4) * cs +
                      (size_t)capE * 4;
   if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
   if (rows * wg > INT32_MAX) return FDWT_ERR_ARG;
