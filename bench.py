@@ -225,6 +225,17 @@ def attention_cpu(batch=1, reps=3):
                       f"and w0, median of {reps} after 1 warm-up ({t:.2f} s per step)"}
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` on this workload, as measured by the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated against a plain copy), or None."""
+    path = os.path.join(ROOT, "profiles", "dwt_sweep_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)[kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -289,7 +300,7 @@ def main():
     dom = max(kernels, key=lambda k: kernels[k]["launches"] * kernels[k]["mean_ms"])
     ach = kernels[dom]["gbps"]
     roofline = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "frac": ach / (HBM_PEAK / 1e9), "traffic": None,
+                "unit": "GB/s", "frac": ach / (HBM_PEAK / 1e9), "traffic": measured_traffic(dom),
                 "alg_bytes_per_launch": kernels[dom]["alg_bytes"],
                 "mean_launch_ms": kernels[dom]["mean_ms"]}
 
