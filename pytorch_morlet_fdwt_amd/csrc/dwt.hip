@@ -118,7 +118,8 @@ __host__ __device__ inline LevelGeom level_geom(int nc, int m, int ncn, bool las
   const int nleft = g.md == FDWT_MODE_ZERO ? 0 : (g.pmin < 0 ? -g.pmin : 0);
   const int nright = g.md == FDWT_MODE_ZERO ? 0 : (g.pmax - m + 1 > 0 ? g.pmax - m + 1 : 0);
   const int nextra = nleft + nright;
-  g.band = nextra ? nextra + 2 : 0;
+  // fold targets lie within max(nleft, nright) + 1 positions of either end
+  g.band = nextra ? (nleft > nright ? nleft : nright) + 2 : 0;
   g.small = m <= 2 * g.band;
   g.nb = nextra ? (g.small ? m : 2 * g.band) : 0;
   g.mw = last ? m : (ncn < m ? ncn : m);  // positions the next level reads
@@ -159,10 +160,6 @@ __device__ inline RLevel load_rlevel(const RLevel* p) {
     w[4 * k + 3] = __builtin_amdgcn_readfirstlane(t.w);
   }
   return r;
-}
-
-__host__ __device__ inline int floor_div(int a, int b) {  // b > 0
-  return a >= 0 ? a / b : -((-a + b - 1) / b);
 }
 
 // Per-level parameters of the synthesis chain as the kernel keeps them in LDS (64 bytes).
@@ -904,17 +901,17 @@ __device__ inline T synthesis_lds_point(const T* a0, const T* dp, int p, int off
   if constexpr (LT > 0) {
     // both parities with constant tap indices (a tap chosen by the lane's parity would need
     // the register-held taps indexed at run time), then the lane's parity selects
-    T ze = T(0), zo = T(0);
+    T ze = T(0), zo = T(0), ze2 = T(0), zo2 = T(0);  // two chains per parity
 #pragma unroll
     for (int t = 0; t < LT / 2; ++t) {
       const T av = a0[u + t];
       const T dv = dp[u + t];
       ze = fma(h0[2 * t], av, ze);
-      ze = fma(h1[2 * t], dv, ze);
+      ze2 = fma(h1[2 * t], dv, ze2);
       zo = fma(h0[2 * t + 1], av, zo);
-      zo = fma(h1[2 * t + 1], dv, zo);
+      zo2 = fma(h1[2 * t + 1], dv, zo2);
     }
-    z = par ? zo : ze;
+    z = par ? zo + zo2 : ze + ze2;
   } else {
     for (int t = 0; t < L / 2; ++t) {
       z = fma(h0[2 * t + par], a0[u + t], z);
@@ -939,13 +936,14 @@ __device__ inline T band_sum(int i, int lo, int hi, int m, int md, int P, int pm
   else if (md == FDWT_MODE_PERIODIZATION && i == m - 1 && P > m) mirror = m;
   const int a = lo > pmin ? lo : pmin;
   const int b = hi < pmax + 1 ? hi : pmax + 1;
+  // walk each residue class up from its base and down from base - P (no division)
   for (int w = 0; w < 2; ++w) {
     const int base = w == 0 ? i : mirror;
     if (base < 0) continue;
-    for (int k = floor_div(a - base + P - 1, P); base + k * P < b; ++k) {
-      const int p = base + k * P;
-      if (p < 0 || p >= m) s += synthesis_lds_point<T, LT>(a0, dp, p, off, h0, h1, L);
-    }
+    for (int p = base; p < b; p += P)
+      if ((p < 0 || p >= m) && p >= a) s += synthesis_lds_point<T, LT>(a0, dp, p, off, h0, h1, L);
+    for (int p = base - P; p >= a; p -= P)
+      if (p < b) s += synthesis_lds_point<T, LT>(a0, dp, p, off, h0, h1, L);
   }
   return s;
 }
@@ -1118,7 +1116,22 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
     T acc[BK];
 #pragma unroll
     for (int j = 0; j < BK; ++j) acc[j] = T(0);
-    const int bt = NT - 1 - tid;  // band lane index
+    // band lane index of this thread (NT * BK: none).  With band <= 64 the left band runs
+    // on the top wave and the right band on the wave below it; otherwise band position b
+    // runs on lane NT - 1 - (b mod NT).
+    int bt = NT * BK;
+    {
+      const int wv = tid >> 6, ln = 63 - (tid & 63);
+      if (lr.band <= 64) {
+        if (wv == NT / 64 - 1) {
+          if (ln < lr.band) bt = ln;
+        } else if (wv == NT / 64 - 2) {
+          bt = lr.band + ln;
+        }
+      } else {
+        bt = NT - 1 - tid;
+      }
+    }
 
     for (int pi = 0; pi < lr.npass; ++pi) {
       const int pb = lr.ub0 + pi * PS;
@@ -1182,12 +1195,17 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
 
       // band lanes: the positions of this pass that fold onto band positions
       if (bt < lr.nb) {
+        // the band lane index passes through an empty asm statement so that the compiler
+        // keeps this lane-specific set-up inside the branch (hoisted out of the pass loop it
+        // would run in every lane of every level)
+        int bo = bt;
+        asm volatile("" : "+v"(bo));
         const int q0 = 2 * pb + off - 1;
         const int lo = max(q0, lr.pbeg);
         const int hi = min(q0 + 2 * PS, lr.pend);
 #pragma unroll
         for (int j = 0; j < BK; ++j) {
-          const int b = bt + j * NT;
+          const int b = bo + j * NT;
           if (b < lr.nb) {
             const int i = (lr.small || b < lr.band) ? b : m - 2 * lr.band + b;
             acc[j] += band_sum<T, LT>(i, lo, hi, m, lr.md, lr.P, lr.pmin, lr.pmax, a0, dp, off,
@@ -1197,9 +1215,11 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
       }
     }
     if (bt < lr.nb) {
+      int bo = bt;
+      asm volatile("" : "+v"(bo));
 #pragma unroll
       for (int j = 0; j < BK; ++j) {
-        const int b = bt + j * NT;
+        const int b = bo + j * NT;
         if (b < lr.nb) {
           const int i = (lr.small || b < lr.band) ? b : m - 2 * lr.band + b;
           if (i < lr.mw) {
