@@ -30,7 +30,10 @@ constexpr int GA = 2;            // thread groups per analysis chunk
 constexpr int CO = NT * VA * GA; // outputs per analysis chunk (2048)
 constexpr int VS = 2;            // consecutive synthesis pairs (u values) per thread
 constexpr int GS = 5;            // thread groups per synthesis pass
-constexpr int PS = NT * VS * GS; // coefficient pairs per synthesis pass (4096)
+constexpr int PS = NT * VS * GS; // coefficient pairs per synthesis pass (split kernel)
+constexpr int VR = 4;            // consecutive synthesis pairs per thread (whole-row kernel)
+constexpr int GR = 3;            // thread groups per pass (whole-row kernel)
+constexpr int PR = NT * VR * GR; // coefficient pairs per pass of the whole-row kernel (6144)
 constexpr int QR = 16;           // queue registers per thread (queue <= QR * NT samples)
 constexpr int MAXL_T = 32;       // largest templated filter length
 constexpr int MAX_TAPS = 256;    // longest filter accepted (PyWavelets' longest is 102)
@@ -128,9 +131,9 @@ __host__ __device__ inline LevelGeom level_geom(int nc, int m, int ncn, bool las
   g.phi = g.small ? 0 : (hi < g.mw ? hi : g.mw);
   g.pbeg = nextra ? (g.pmin < 0 ? g.pmin : 0) : 0;
   g.pend = nextra ? (g.pmax + 1 > m ? g.pmax + 1 : m) : g.mw;
-  g.ub0 = ((g.pbeg + 1 - off) >> 1) & ~(VS - 1);
+  g.ub0 = ((g.pbeg + 1 - off) >> 1) & ~(VR - 1);
   const int first = 2 * g.ub0 + off - 1;
-  g.npass = g.pend > first ? (g.pend - first + 2 * PS - 1) / (2 * PS) : 0;
+  g.npass = g.pend > first ? (g.pend - first + 2 * PR - 1) / (2 * PR) : 0;
   return g;
 }
 
@@ -247,18 +250,18 @@ __device__ inline void analysis_pair(const T* __restrict__ s, const T* hr0, cons
 // z_odd[q] (position off + 2(u0+q) - 1) and z_even[q] (position off + 2(u0+q)) from the
 // low band a[0..] and the high band d[0..], both LDS windows starting at coefficient u0
 // (16-byte aligned, zero outside the coefficients).
-template <typename T, int LT>
+template <typename T, int LT, int V = VS>
 __device__ inline void synthesis_block(const T* __restrict__ a, const T* __restrict__ d,
-                                       const T* h0, const T* h1, int L, T (&zo)[VS],
-                                       T (&ze)[VS]) {
+                                       const T* h0, const T* h1, int L, T (&zo)[V],
+                                       T (&ze)[V]) {
   if constexpr (LT > 0) {
     constexpr int H = LT / 2;
-    constexpr int W = VS + H - 1;
+    constexpr int W = V + H - 1;
     T av[W], dv[W];
-    lds_window<VS>(a, av);  // windows start VS elements apart (VS-aligned)
-    lds_window<VS>(d, dv);
+    lds_window<(V >= 4 && sizeof(T) == 4) ? 4 : 2>(a, av);  // windows start V elements apart
+    lds_window<(V >= 4 && sizeof(T) == 4) ? 4 : 2>(d, dv);
 #pragma unroll
-    for (int q = 0; q < VS; ++q) {
+    for (int q = 0; q < V; ++q) {
       T so = T(0), se = T(0);
 #pragma unroll
       for (int t = 0; t < H; ++t) {
@@ -273,7 +276,7 @@ __device__ inline void synthesis_block(const T* __restrict__ a, const T* __restr
   } else {
     const int H = L / 2;
 #pragma unroll
-    for (int q = 0; q < VS; ++q) {
+    for (int q = 0; q < V; ++q) {
       T so = T(0), se = T(0);
       for (int t = 0; t < H; ++t) {
         const T av = a[q + t];
@@ -889,6 +892,42 @@ __global__ void __launch_bounds__(NT) synthesis_chain_kernel(SChainArgs args, in
   }
 }
 
+// Store the 2 VR consecutive values v of positions i0.. of a wave whose lanes hold
+// consecutive runs, as 16-byte blocks starting at i0 + sh (16-byte aligned): each lane stores
+// v[sh..] and the first sh values of the next lane; lane 0 also stores its first sh values and
+// lane 63, whose next lane is in another wave, stores its own values one by one.
+template <int SH>
+__device__ inline void store_shifted_sh(float* orow, int i0, const float (&v)[2 * VR],
+                                        int lane) {
+  float nx[SH > 0 ? SH : 1];
+#pragma unroll
+  for (int j = 0; j < SH; ++j) nx[j] = __shfl_down(v[j], 1);
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < SH; ++j) orow[i0 + j] = v[j];
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int j = SH; j < 2 * VR; ++j) orow[i0 + j] = v[j];
+    return;
+  }
+  float w[2 * VR];
+#pragma unroll
+  for (int j = 0; j < 2 * VR; ++j) w[j] = j + SH < 2 * VR ? v[j + SH] : nx[j + SH - 2 * VR];
+  typedef float v4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int q = 0; q < VR / 2; ++q)
+    *reinterpret_cast<v4*>(orow + i0 + SH + 4 * q) =
+        v4{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]};
+}
+
+__device__ inline void store_shifted(float* orow, int i0, const float (&v)[2 * VR], int sh,
+                                     int lane) {
+  if (sh == 1) store_shifted_sh<1>(orow, i0, v, lane);
+  else if (sh == 2) store_shifted_sh<2>(orow, i0, v, lane);
+  else store_shifted_sh<3>(orow, i0, v, lane);
+}
+
 // Value z(p) of one synthesis position from LDS: the low band a0[u] (zero margins) and the
 // high band dp[u] (this pass's window), z(p) = sum_t h0[2t+par] a[u+t] + h1[2t+par] d[u+t].
 template <typename T, int LT>
@@ -1015,7 +1054,7 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
     r.pbeg = g.pbeg;
     r.pend = g.pend;
     const int cap_dst = (l % 2 == 0) ? args.capB : args.capA;  // level l writes B if l even
-    const int zend = ZL + r.ncn + L + 2 * VS + 16;
+    const int zend = ZL + r.ncn + L + 2 * VR + 16;
     r.zend = last ? 0 : (zend < cap_dst ? zend : cap_dst);
     r.small = g.small;
     r.pad = 0;
@@ -1028,8 +1067,8 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
 
   // Prefetch registers hold raw coefficients; the loads are issued here and range-masked and
   // converted only when staged, so no wait follows a load where it is issued.
-  const int dspan = PS + H + 4;
-  constexpr int PFD = PS / NT + 1;  // dspan <= PFD * NT since H + 4 <= NT
+  const int dspan = PR + H + 4;
+  constexpr int PFD = PR / NT + 1;  // dspan <= PFD * NT since H + 4 <= NT
   S pf[PFD] = {};
   auto fetch_d = [&](const S* dr, int ncl, int pbl) {
     if (!dr) return;
@@ -1065,7 +1104,7 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
     const int nc = args.nc[0];
     const S* ag = args.approx ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
     constexpr int AB = 9;
-    const int kend = min(args.capA, ZL + nc + L + 2 * VS + 16);
+    const int kend = min(args.capA, ZL + nc + L + 2 * VR + 16);
     for (int k0 = tid; k0 < kend; k0 += AB * NT) {
       S v[AB] = {};
       if (ag) {
@@ -1113,6 +1152,11 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
     // multiple of 4, and m % 4 == 0 keeps rows 16-byte aligned in global memory
     const bool vec_out = std::is_same<S, float>::value && off == 1 && (m % 4) == 0;
     const bool vec_lds = off == 1;
+    // other offsets put a thread's first position sh short of a 16-byte boundary: whole
+    // waves inside the plain range then store 16-byte blocks shifted by sh positions, taking
+    // the last sh values of each block from the next lane
+    const int sh = (4 - ((off - 1) & 3)) & 3;
+    const bool vec_shift = std::is_same<S, float>::value && last && sh != 0 && (m % 4) == 0;
     T acc[BK];
 #pragma unroll
     for (int j = 0; j < BK; ++j) acc[j] = T(0);
@@ -1134,7 +1178,7 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
     }
 
     for (int pi = 0; pi < lr.npass; ++pi) {
-      const int pb = lr.ub0 + pi * PS;
+      const int pb = lr.ub0 + pi * PR;
       const T* dp;  // dp[u] = high band coefficient u (this pass's window)
       if (lr.qoff >= 0) {
         dp = D + lr.qoff - lr.ub0;
@@ -1149,7 +1193,7 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
         }
         __syncthreads();
         if (pi + 1 < lr.npass) {
-          fetch_d(drow, nc, pb + PS);
+          fetch_d(drow, nc, pb + PR);
         } else if (!last) {
           const RLevel nr = load_rlevel(lrec + l + 1);
           if (nr.qoff < 0) fetch_d(static_cast<const S*>(nr.drow), nr.nc, nr.ub0);
@@ -1159,32 +1203,42 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
 
       // main pass: positions [plo, phi)
 #pragma unroll
-      for (int g = 0; g < GS; ++g) {
-        const int lu = (g * NT + tid) * VS;  // coefficient offset inside the pass
+      for (int g = 0; g < GR; ++g) {
+        const int lu = (g * NT + tid) * VR;  // coefficient offset inside the pass
         const int ub = pb + lu;
-        const int i0 = 2 * ub + off - 1;     // first of this thread's 2 * VS positions
-        if (i0 + 2 * VS <= lr.plo || i0 >= lr.phi) continue;
-        T zo[VS], ze[VS];
-        synthesis_block<T, LT>(a0 + ub, dp + ub, h0, h1, L, zo, ze);
-        T v[2 * VS];
+        const int i0 = 2 * ub + off - 1;     // first of this thread's 2 * VR positions
+        if (i0 + 2 * VR <= lr.plo || i0 >= lr.phi) continue;
+        T zo[VR], ze[VR];
+        synthesis_block<T, LT, VR>(a0 + ub, dp + ub, h0, h1, L, zo, ze);
+        T v[2 * VR];
 #pragma unroll
-        for (int q = 0; q < VS; ++q) {
+        for (int q = 0; q < VR; ++q) {
           v[2 * q] = zo[q];
           v[2 * q + 1] = ze[q];
         }
-        if (VS == 2 && i0 >= lr.plo && i0 + 2 * VS <= lr.phi && (last ? vec_out : vec_lds)) {
+        if constexpr (std::is_same<S, float>::value) {
+          const int iw = i0 - 2 * VR * (tid & 63);  // first position of the wave
+          if (vec_shift && iw >= lr.plo && iw + 128 * VR <= lr.phi) {
+            store_shifted(orow, i0, v, sh, tid & 63);
+            continue;
+          }
+        }
+        if (i0 >= lr.plo && i0 + 2 * VR <= lr.phi && (last ? vec_out : vec_lds)) {
           typedef T v4 __attribute__((ext_vector_type(4)));
-          const v4 w = {v[0], v[1], v[2], v[3]};
-          if (last) {
-            if constexpr (std::is_same<S, float>::value)
-              *reinterpret_cast<v4*>(orow + i0) = w;
-          } else {
-            *reinterpret_cast<v4*>(dst + ZL + i0) = w;
+#pragma unroll
+          for (int q = 0; q < VR / 2; ++q) {
+            const v4 w = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            if (last) {
+              if constexpr (std::is_same<S, float>::value)
+                *reinterpret_cast<v4*>(orow + i0 + 4 * q) = w;
+            } else {
+              *reinterpret_cast<v4*>(dst + ZL + i0 + 4 * q) = w;
+            }
           }
           continue;
         }
 #pragma unroll
-        for (int j = 0; j < 2 * VS; ++j) {
+        for (int j = 0; j < 2 * VR; ++j) {
           const int i = i0 + j;
           if (i >= lr.plo && i < lr.phi) {
             if (last) Storage<S>::store(orow, i, v[j]);
@@ -1202,7 +1256,7 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
         asm volatile("" : "+v"(bo));
         const int q0 = 2 * pb + off - 1;
         const int lo = max(q0, lr.pbeg);
-        const int hi = min(q0 + 2 * PS, lr.pend);
+        const int hi = min(q0 + 2 * PR, lr.pend);
 #pragma unroll
         for (int j = 0; j < BK; ++j) {
           const int b = bo + j * NT;
@@ -1424,6 +1478,14 @@ extern "C" int64_t fdwt_chain_max_length(int32_t taps, int32_t dtype) {
   int64_t n = 2 * (budget - stage - 6 * (int64_t)taps);
   const int64_t n2 = (budget - 6 * (int64_t)taps) * 4 / 3;
   if (n2 / 4 > stage) n = n2;  // the n/4 term dominates the staging window
+  // synthesis (whole-row kernel): level table + outputs n/2 and n/4 with margins + the pass
+  // window D + taps
+  const int64_t zl = (taps + 3) & ~3;
+  const int64_t margin = zl + taps + 2 * VR + 24 + 4;
+  const int64_t sbudget = (160 * 1024 - RLEVEL_BYTES) / compute_size(dtype) - 2 * margin -
+                          (PR + taps / 2 + 12) - 2 * (int64_t)taps - 8;
+  const int64_t ns = sbudget * 4 / 3 - 8;
+  if (ns < n) n = ns;
   return n > 0 ? n : 0;
 }
 
@@ -1493,9 +1555,9 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
   a.mode = mode;
   a.off = off;
   const int64_t zl = (L + 3) & ~3;
-  const int64_t margin = zl + L + 2 * VS + 24;
+  const int64_t margin = zl + L + 2 * VR + 24;
   int64_t capA = s.nc[0] + margin, capB = 4;
-  const int64_t capD = (PS + L / 2 + 8 + 3) & ~3;
+  const int64_t capD = (PR + L / 2 + 8 + 3) & ~3;
   int slot = 0;
   int64_t qpos = 0;
   bool queue_open = true;
@@ -1515,7 +1577,7 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
     // the queue takes a prefix of the levels (never the last), each a single pass
     if (queue_open && !last) {
       const int64_t ub_last = (g.pend - off) >> 1;
-      const int64_t len = ub_last - g.ub0 + 2 * VS + L / 2 + 4;
+      const int64_t len = ub_last - g.ub0 + 2 * VR + L / 2 + 4;
       const int ns = (int)cdiv(len, NT);
       if (g.npass != 1 || slot + ns > QR || qpos + len > capD) {
         queue_open = false;

@@ -199,6 +199,40 @@ def test_long_rows_and_few_rows():
                                                         "reflect"), atol=1e-5, rtol=1e-5)
 
 
+def test_chains_at_the_on_chip_limit():
+    """Rows exactly as long as the on-chip chain allows (fp32, 16 and 18 taps): the fused
+    analysis and synthesis chains of all levels run with LDS close to full."""
+    from pytorch_morlet_fdwt_amd import _lib
+    for w, taps in (("sym8", 16), ("coif3", 18)):
+        n = _lib.lib().fdwt_chain_max_length(taps, 0)
+        x = _rand((2, n), 7, torch.float32)
+        for mode in ("symmetric", "periodization"):
+            c = fdwt.wavedec(x.to(DEV), w, mode, 4)
+            r = O.wavedec(x.double(), w, mode, 4)
+            for a, b in zip(c, r):
+                torch.testing.assert_close(a.cpu().double(), b, atol=1e-5, rtol=1e-5)
+            rec = fdwt.waverec(c, w, mode)
+            ref = O.waverec([t.cpu().double() for t in c], w, mode)
+            torch.testing.assert_close(rec.cpu().double(), ref, atol=2e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("wavelet", ["db1", "db2", "db3", "db4", "sym8", "coif3", "bior3.5"])
+def test_periodization_reconstruction_all_offsets(wavelet):
+    """Periodization shifts every synthesis position by L/2 - 1, so its outputs sit at each
+    offset modulo 4 across these filter lengths (2 .. 18); long fp32 rows exercise the vector
+    stores of whole waves."""
+    for n in (4099, 4100, 6000):
+        x = _rand((3, n), 8, torch.float32)
+        c = fdwt.wavedec(x.to(DEV), wavelet, "periodization", 3)
+        rec = fdwt.waverec(c, wavelet, "periodization")
+        ref = O.waverec([t.cpu().double() for t in c], wavelet, "periodization")
+        torch.testing.assert_close(rec.cpu().double(), ref, atol=2e-5, rtol=1e-5)
+        a, d = fdwt.dwt(x.to(DEV), wavelet, "periodization")
+        y = fdwt.idwt(a, d, wavelet, "periodization")
+        yr = O.idwt(a.cpu().double(), d.cpu().double(), wavelet, "periodization")
+        torch.testing.assert_close(y.cpu().double(), yr, atol=2e-5, rtol=1e-5)
+
+
 def test_edge_cases():
     e = torch.empty(0, 5, 100, device=DEV)
     a, d = fdwt.dwt(e, "db4")
