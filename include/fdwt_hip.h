@@ -37,6 +37,7 @@ extern "C" {
 #define FDWT_ERR_ARG (-1)         /* invalid size / mode / dtype / null pointer */
 #define FDWT_ERR_TOO_LONG (-2)    /* a row does not fit the kernel's on-chip buffers */
 #define FDWT_MAX_LEVELS 32
+#define FDWT_SYN_MAX_LEVELS 16   /* levels per fdwt_synthesis_chain call */
 
 /* Error message for a return code of this library (or a hipError_t). */
 const char* fdwt_error_string(int code);
@@ -86,7 +87,8 @@ int fdwt_analysis_chain(const void* x, void* const* details, void* approx, const
  * details[l] (length nc[l]; NULL = zeros) into a signal of length n_out[l].  The low band
  * of level 0 is approx (NULL = zeros); the low band of level l > 0 is the first nc[l]
  * samples of the output of level l - 1 (nc[l] is n_out[l-1] or n_out[l-1] - 1, the
- * pywt.waverec trim).  out receives the output of the last level.
+ * pywt.waverec trim).  out receives the output of the last level.  At most
+ * FDWT_SYN_MAX_LEVELS levels per call (longer chains run as consecutive calls).
  */
 int fdwt_synthesis_chain(const void* approx, const void* const* details, void* out,
                          const void* h0, const void* h1, int64_t rows, const int64_t* nc,

@@ -79,89 +79,188 @@ struct SChainArgs {
   int32_t qlevels;
 };
 
-// Arguments of the whole-row synthesis chain (one workgroup per row).  The "queue" holds the
-// high bands of the first qlevels levels (each a single pass): at kernel start, queue slot k
-// loads coefficients qs_u0[k] .. qs_u0[k] + NT - 1 of band qs_ptr[k] (rows of qs_nc[k]) into
-// registers and then stages the first qs_len[k] of them at D[qs_pos[k] ..]; level l < qlevels
-// finds its band at D[qoff[l] + u - ub0].  Later levels stream their high band pass by pass.
-struct RChainArgs {
-  const void* approx;
-  const void* details[FDWT_MAX_LEVELS];
-  void* out;
-  const void* h0;
-  const void* h1;
-  int32_t nc[FDWT_MAX_LEVELS];
-  int32_t n_out[FDWT_MAX_LEVELS];
-  int32_t qoff[FDWT_MAX_LEVELS];
-  int32_t levels, taps, mode, off;
-  int32_t capA, capB, capD;
-  int32_t qslots, qlevels;
-  const void* qs_ptr[QR];
-  int32_t qs_nc[QR];
-  int32_t qs_u0[QR];
-  int32_t qs_pos[QR];
-  int32_t qs_len[QR];
+// ------------------------------------------------------------------ persistent synthesis: plan
+// The whole-row synthesis kernel (one workgroup per row at a time, rows blockIdx.x,
+// blockIdx.x + gridDim.x, ...) keeps the low band of every level in LDS and reads each band of
+// a row from HBM exactly once, into prefetch registers, well before it is used.  A prefetch
+// register holds up to NT consecutive coefficients of one band (lane t the t-th of them).  Two
+// register sets:
+//  * the head (PA registers): every band of the levels before the last (a_0, d_0 .. d_{J-2}),
+//    requested for the next row just before the current row's last level runs;
+//  * the tail (PB registers): the last level's band(s), requested at the start of the row, so
+//    that it arrives while levels 0 .. J-2 run.
+// The kernel waits for outstanding loads explicitly at two points only (the start of a row and
+// the start of its last level); in between, staging reads registers whose loads are known to
+// be complete, so the compiler adds no wait of its own.  Rows whose bands do not fit the sets
+// load each band at its level instead (no prefetch).
+constexpr int PA = 24;  // head prefetch registers per thread
+constexpr int PB = 20;  // tail prefetch registers per thread
+
+// LDS buffers of the whole-row synthesis kernel, in this order (element offsets P, Q, D, E,
+// T): the low band of level l lives in P when J - 1 - l is even and in Q otherwise (the last
+// level reads P); the high band of levels < J - 1 is staged in D and the last level's high
+// band across Q and D, which hold nothing live by then.  E holds the positions parked for the
+// boundary fold, T the taps of runtime-length filters.
+inline int syn_src(int l, int J, int P, int Q) { return ((J - 1 - l) & 1) ? Q : P; }
+inline int syn_dbuf(int l, int J, int Q, int D) { return l == J - 1 ? Q : D; }
+
+// Geometry of one synthesis level.  The level produces z(p) for the extended positions
+// p in [pbeg, pend) from the coefficient pairs v in [vbeg, vend) (pair v gives positions
+// 2v + off - 1 and 2v + off).  Positions in [plo, phi) are written as they are; the others are
+// parked in E and, after the level, every fold target i in [0, plo) or [phi, mw) receives the
+// sum of the parked values of the positions that the mode's extension maps onto it.  Zero
+// mode folds nothing (plo = 0, phi = mw).  mw = positions the next level reads (all m on the
+// last level).  The level reads coefficients [vbeg - .., zhi) of both bands (zero outside the
+// band).
+struct SynGeom {
+  int m, mw, md, P, pbeg, pend, plo, phi, vbeg, vend, zhi, ne, nt;
 };
 
-// Geometry of one synthesis level (shared by the host and the kernel).  Outputs positions
-// [0, m) from nc coefficient pairs; positions outside [0, m) fold back onto "band" positions
-// near the ends (none in zero mode).  The passes run over coefficient pairs ub0, ub0 + PS, ..
-// and cover the positions [pbeg, pend).
-struct LevelGeom {
-  int md, P, pmin, pmax, band, nb, small, mw, plo, phi, pbeg, pend, ub0, npass;
-};
+__host__ __device__ inline int floor_div(int a, int b) {
+  return a >= 0 ? a / b : -((-a + b - 1) / b);
+}
 
-__host__ __device__ inline LevelGeom level_geom(int nc, int m, int ncn, bool last, int L,
-                                                int off, int mode) {
-  LevelGeom g;
+__host__ __device__ inline SynGeom syn_geom(int nc, int m, int ncn, bool last, int L, int off,
+                                            int mode) {
+  SynGeom g;
+  g.m = m;
   g.md = normalize_mode(mode, m);
   g.P = mode_period(g.md, m);
-  g.pmin = off - (L - 1);
-  g.pmax = 2 * (nc - 1) + off;
-  const int nleft = g.md == FDWT_MODE_ZERO ? 0 : (g.pmin < 0 ? -g.pmin : 0);
-  const int nright = g.md == FDWT_MODE_ZERO ? 0 : (g.pmax - m + 1 > 0 ? g.pmax - m + 1 : 0);
-  const int nextra = nleft + nright;
-  // fold targets lie within max(nleft, nright) + 1 positions of either end
-  g.band = nextra ? (nleft > nright ? nleft : nright) + 2 : 0;
-  g.small = m <= 2 * g.band;
-  g.nb = nextra ? (g.small ? m : 2 * g.band) : 0;
-  g.mw = last ? m : (ncn < m ? ncn : m);  // positions the next level reads
-  g.plo = g.small ? m : g.band;           // positions written by the main pass: [plo, phi)
-  const int hi = m - g.band;
-  g.phi = g.small ? 0 : (hi < g.mw ? hi : g.mw);
-  g.pbeg = nextra ? (g.pmin < 0 ? g.pmin : 0) : 0;
-  g.pend = nextra ? (g.pmax + 1 > m ? g.pmax + 1 : m) : g.mw;
-  g.ub0 = ((g.pbeg + 1 - off) >> 1) & ~(VR - 1);
-  const int first = 2 * g.ub0 + off - 1;
-  g.npass = g.pend > first ? (g.pend - first + 2 * PR - 1) / (2 * PR) : 0;
+  g.mw = last ? m : (ncn < m ? ncn : m);
+  const int pmin = off - (L - 1);
+  const int pmax = 2 * (nc - 1) + off;
+  if (g.md == FDWT_MODE_ZERO) {
+    g.pbeg = 0;
+    g.pend = g.mw;
+    g.plo = 0;
+    g.phi = g.mw;
+  } else {
+    const int nleft = pmin < 0 ? -pmin : 0;
+    const int nright = pmax - m + 1 > 0 ? pmax - m + 1 : 0;
+    // every extended position folds onto a position within max(nleft, nright) + 1 of an end
+    const int band = (nleft > nright ? nleft : nright) + 2;
+    g.pbeg = pmin < 0 ? pmin : 0;
+    g.pend = pmax + 1 > m ? pmax + 1 : m;
+    if (m <= 2 * band) {
+      g.plo = m;
+      g.phi = m;
+    } else {
+      g.plo = band;
+      g.phi = m - band < g.mw ? m - band : g.mw;
+      if (g.phi < g.plo) g.phi = g.plo;
+    }
+  }
+  g.ne = (g.plo - g.pbeg) + (g.pend - g.phi);
+  const int nl = g.plo < g.mw ? g.plo : g.mw;
+  g.nt = nl + (g.mw > g.phi ? g.mw - g.phi : 0);
+  g.vbeg = floor_div(floor_div(g.pbeg - off + 1, 2), VR) * VR;
+  g.vend = floor_div(g.pend - off, 2) + 1;
+  if (g.vend < g.vbeg) g.vend = g.vbeg;
+  g.zhi = (((g.vend > nc ? g.vend : nc) + VR + L / 2 + 4) + 3) & ~3;
   return g;
 }
 
-// Per-level record of the whole-row synthesis kernel, kept in LDS (96 bytes).
-struct RLevel {
-  int32_t nc, m, mw, ncn;
-  int32_t ub0, npass, qoff, md;
-  int32_t P, pmin, pmax, band;
-  int32_t nb, plo, phi, pbeg;
-  int32_t pend, zend, small, pad;
-  const void* drow;
-  int32_t pad2[2];
+// Per-level record of the kernel (80 bytes).
+struct SynLevel {
+  int32_t m, mw, md, P;
+  int32_t pbeg, pend, plo, phi;
+  int32_t vbeg, vend, zhi, nt;
+  int32_t src, dst, dbuf, nva;  // buffer offsets (dst -1 on the last level); valid low-band
+  int32_t nvd, pad[3];          // coefficients; valid high-band coefficients
 };
-constexpr int RLEVEL_BYTES = FDWT_MAX_LEVELS * (int)sizeof(RLevel);
 
-__device__ inline RLevel load_rlevel(const RLevel* p) {
+// One prefetch register: up to NT consecutive coefficients of one band, lane t holding the
+// t-th; its load descriptor (16 bytes) and staging word.
+struct SynLoad {
+  const void* base;  // lane 0's coefficient in row 0
+  int32_t stride;    // bytes per row of the band
+  int32_t cnt;       // coefficients held (0: register unused)
+};
+// Staging word of a prefetch register: LDS element offset of lane 0's coefficient | count << 18.
+__host__ __device__ inline uint32_t syn_stage_word(int dest, int cnt) {
+  return (uint32_t)dest | ((uint32_t)cnt << 18);
+}
+
+// Arguments of the whole-row synthesis kernel.  Every table the kernel reads per level or per
+// register lives here, so it reaches the kernel through scalar loads of the kernel arguments
+// (no vector instruction spent on it).
+struct SynArgs {
+  // band[0] = the coarsest approximation, band[l + 1] = the details of level l (one array: a
+  // run-time choice between two argument fields would make the compiler copy the arguments to
+  // private memory)
+  const void* band[FDWT_SYN_MAX_LEVELS + 1];
+  void* out;
+  const void* h0;
+  const void* h1;
+  int64_t rows;
+  int32_t nc[FDWT_SYN_MAX_LEVELS];
+  int32_t levels, taps, off, prefetch;  // prefetch: the bands fit the head and tail registers
+  int32_t offE, offTap;
+  uint32_t maskA[FDWT_SYN_MAX_LEVELS];  // head registers staged at each level
+  SynLevel lv[FDWT_SYN_MAX_LEVELS];
+  SynLoad ldA[PA];  // head registers
+  SynLoad ldB[PB];  // tail registers
+  uint32_t stA[PA];
+  uint32_t stB[PB];
+};
+
+// The prefetch registers of a row: each band of the head (a_0, d_0 .. d_{J-2} when J > 1)
+// and of the tail (d_{J-1}, or a_0 and d_0 when J == 1) takes ceil(count / NT) registers of
+// its set.  emit(tail, k, c0, cnt, dest, level, is_approx) is called for each register;
+// returns false when a set overflows (then nothing is prefetched).
+template <typename F>
+inline bool syn_regs(int J, const int32_t* nc, const void* approx, const void* const* details,
+                     int ZL, int yP, int yQ, int yD, F&& emit) {
+  int ka = 0, kb = 0;
+  for (int s = 0; s <= J; ++s) {
+    const int l = s == 0 ? 0 : s - 1;
+    const void* ptr = s == 0 ? approx : details[l];
+    const int cnt = nc[l];
+    if (!ptr || cnt <= 0) continue;
+    const bool tail = l == J - 1;
+    const int dest = (s == 0 ? syn_src(0, J, yP, yQ) : syn_dbuf(l, J, yQ, yD)) + ZL;
+    for (int c0 = 0; c0 < cnt; c0 += NT) {
+      int& k = tail ? kb : ka;
+      if (k == (tail ? PB : PA)) return false;
+      emit(tail, k, c0, cnt - c0 < NT ? cnt - c0 : NT, dest + c0, l, s == 0);
+      ++k;
+    }
+  }
+  return true;
+}
+
+// Load element i of a global array whose pointer the compiler cannot place in the global
+// address space (e.g. one read from LDS): a generic (flat) load would also count against the
+// LDS wait counter, so every later LDS wait would wait for it too.
+template <typename S>
+__device__ inline S global_load(const S* p, int64_t i) {
+  typedef typename std::conditional<
+      sizeof(S) == 2, uint16_t,
+      typename std::conditional<sizeof(S) == 4, uint32_t, uint64_t>::type>::type U;
+  typedef __attribute__((address_space(1))) const U* gptr;
+  const U u = ((gptr)p)[i];
+  S v;
+  __builtin_memcpy(&v, &u, sizeof(S));
+  return v;
+}
+
+// Read a record that every lane reads at the same LDS address and make it wave-uniform.
+template <typename R>
+__device__ inline R lds_uniform(const R* p) {
+  static_assert(sizeof(R) % 16 == 0, "records are whole 16-byte words");
   typedef int v4i __attribute__((ext_vector_type(4)));
   const v4i* q = reinterpret_cast<const v4i*>(p);
-  RLevel r;
-  int* w = reinterpret_cast<int*>(&r);
+  int w[sizeof(R) / 4];
 #pragma unroll
-  for (int k = 0; k < 6; ++k) {
+  for (int k = 0; k < (int)sizeof(R) / 16; ++k) {
     const v4i t = q[k];
     w[4 * k + 0] = __builtin_amdgcn_readfirstlane(t.x);
     w[4 * k + 1] = __builtin_amdgcn_readfirstlane(t.y);
     w[4 * k + 2] = __builtin_amdgcn_readfirstlane(t.z);
     w[4 * k + 3] = __builtin_amdgcn_readfirstlane(t.w);
   }
+  R r;
+  __builtin_memcpy(&r, w, sizeof(R));
   return r;
 }
 
@@ -928,88 +1027,57 @@ __device__ inline void store_shifted(float* orow, int i0, const float (&v)[2 * V
   else store_shifted_sh<3>(orow, i0, v, lane);
 }
 
-// Value z(p) of one synthesis position from LDS: the low band a0[u] (zero margins) and the
-// high band dp[u] (this pass's window), z(p) = sum_t h0[2t+par] a[u+t] + h1[2t+par] d[u+t].
-template <typename T, int LT>
-__device__ inline T synthesis_lds_point(const T* a0, const T* dp, int p, int off, const T* h0,
-                                        const T* h1, int L) {
-  const int r = p - off;
-  const int par = r & 1;
-  const int u = (r + par) >> 1;
-  T z = T(0);
-  if constexpr (LT > 0) {
-    // both parities with constant tap indices (a tap chosen by the lane's parity would need
-    // the register-held taps indexed at run time), then the lane's parity selects
-    T ze = T(0), zo = T(0), ze2 = T(0), zo2 = T(0);  // two chains per parity
-#pragma unroll
-    for (int t = 0; t < LT / 2; ++t) {
-      const T av = a0[u + t];
-      const T dv = dp[u + t];
-      ze = fma(h0[2 * t], av, ze);
-      ze2 = fma(h1[2 * t], dv, ze2);
-      zo = fma(h0[2 * t + 1], av, zo);
-      zo2 = fma(h1[2 * t + 1], dv, zo2);
-    }
-    z = par ? zo + zo2 : ze + ze2;
-  } else {
-    for (int t = 0; t < L / 2; ++t) {
-      z = fma(h0[2 * t + par], a0[u + t], z);
-      z = fma(h1[2 * t + par], dp[u + t], z);
-    }
-  }
-  return z;
-}
-
-// Sum of z over the extended positions in [lo, hi) that fold onto row position i (i itself
-// when it lies in [lo, hi)): the positions congruent modulo the period P to i and, for the
-// mirroring extensions, to the mirror image of i.
-template <typename T, int LT>
-__device__ inline T band_sum(int i, int lo, int hi, int m, int md, int P, int pmin, int pmax,
-                             const T* a0, const T* dp, int off, const T* h0, const T* h1,
-                             int L) {
-  T s = T(0);
-  if (i >= lo && i < hi) s += synthesis_lds_point<T, LT>(a0, dp, i, off, h0, h1, L);
+// Sum of the parked values of the extended positions that fold onto row position i (i itself
+// included): the positions congruent modulo the period P to i and, for the mirroring
+// extensions, to the mirror image of i.  Parked position p sits at E[p - pbeg] below plo and
+// at E[(plo - pbeg) + (p - phi)] from phi on.
+template <typename T>
+__device__ inline T fold_parked(const T* __restrict__ E, int i, int m, int md, int P, int pbeg,
+                                int pend, int plo, int phi) {
+  auto at = [&](int p) { return E[p < plo ? p - pbeg : (plo - pbeg) + (p - phi)]; };
+  T s = at(i);
   int mirror = -1;
   if (md == FDWT_MODE_SYMMETRIC) mirror = P - 1 - i;
   else if (md == FDWT_MODE_REFLECT && i > 0 && i < m - 1) mirror = P - i;
   else if (md == FDWT_MODE_PERIODIZATION && i == m - 1 && P > m) mirror = m;
-  const int a = lo > pmin ? lo : pmin;
-  const int b = hi < pmax + 1 ? hi : pmax + 1;
   // walk each residue class up from its base and down from base - P (no division)
   for (int w = 0; w < 2; ++w) {
     const int base = w == 0 ? i : mirror;
     if (base < 0) continue;
-    for (int p = base; p < b; p += P)
-      if ((p < 0 || p >= m) && p >= a) s += synthesis_lds_point<T, LT>(a0, dp, p, off, h0, h1, L);
-    for (int p = base - P; p >= a; p -= P)
-      if (p < b) s += synthesis_lds_point<T, LT>(a0, dp, p, off, h0, h1, L);
+    for (int p = base; p < pend; p += P)
+      if (p < 0 || p >= m) s += at(p);
+    for (int p = base - P; p >= pbeg; p -= P)
+      if (p < pend) s += at(p);
   }
   return s;
 }
 
-// Whole-row synthesis chain: one workgroup reconstructs one row through all levels.  The
-// low band lives in LDS (A <-> B ping-pong with zero margins), the high bands are staged in D
-// (the queued small levels once at kernel start, the others pass by pass from prefetch
-// registers).  Each level writes its interior positions from the main pass and the positions
-// near the row ends from "band lanes" (the highest thread ids), which add up every extended
-// position that folds onto them; a level therefore needs no extra fold pass.
-template <typename S, typename T, int LT>
-__global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
+// Whole-row synthesis chain, persistent: each workgroup reconstructs the rows blockIdx.x,
+// blockIdx.x + gridDim.x, .. through all levels (see the plan above).  Per level: the bands
+// prefetched for it are staged into LDS and the buffer margins zeroed; each thread computes
+// VR consecutive coefficient pairs (2 VR positions) at a time from register windows of both
+// bands; positions away from the row ends go straight to the next low band (LDS) or to the
+// output row, the others are parked and folded after a barrier by one lane per fold target.
+template <typename S, typename T, int LT, bool PRE>
+__global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  RLevel* const lrec = reinterpret_cast<RLevel*>(smem_raw);
-  T* const A = reinterpret_cast<T*>(smem_raw + RLEVEL_BYTES);
-  T* const B = A + args.capA;
-  T* const D = B + args.capB;
-  T* const tap_lds = D + args.capD;
-
-  const int64_t row = blockIdx.x;
+  // the arguments, read in place through the kernel-argument segment pointer: scalar loads at
+  // any (wave-uniform) offset, and never a private copy.  (The host compilation pass only
+  // needs the kernel's signature; it sees a plain reference.)
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __attribute__((address_space(4))) const SynArgs KArgs;
+  KArgs& args = *(KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+#else
+  const SynArgs& args = *static_cast<const SynArgs*>(nullptr);
+#endif
+  T* const lds = reinterpret_cast<T*>(smem_raw);
+  const int J = args.levels;
   const int L = LT > 0 ? LT : args.taps;
-  const int H = L / 2;
   const int ZL = (L + 3) & ~3;
   const int off = args.off;
-  const int mode = args.mode;
-  const int levels = args.levels;
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int64_t rows = args.rows;
 
   const T* gh0 = static_cast<const T*>(args.h0);
   const T* gh1 = static_cast<const T*>(args.h1);
@@ -1025,268 +1093,205 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(RChainArgs args) {
     h0 = h0r;
     h1 = h1r;
   } else {
-    load_taps(gh0, gh1, tap_lds, tap_lds + L, L, false);
-    h0 = tap_lds;
-    h1 = tap_lds + L;
+    load_taps(gh0, gh1, lds + args.offTap, lds + args.offTap + L, L, false);
+    h0 = lds + args.offTap;
+    h1 = lds + args.offTap + L;
+    __syncthreads();
   }
 
-  // level table (one lane per level)
-  if (tid < levels) {
-    const int l = tid;
-    const bool last = l + 1 == levels;
-    RLevel r;
-    r.nc = args.nc[l];
-    r.m = args.n_out[l];
-    r.ncn = last ? 0 : args.nc[l + 1];
-    const LevelGeom g = level_geom(r.nc, r.m, r.ncn, last, L, off, mode);
-    r.mw = g.mw;
-    r.ub0 = g.ub0;
-    r.npass = g.npass;
-    r.qoff = args.qoff[l];
-    r.md = g.md;
-    r.P = g.P;
-    r.pmin = g.pmin;
-    r.pmax = g.pmax;
-    r.band = g.band;
-    r.nb = g.nb;
-    r.plo = g.plo;
-    r.phi = g.phi;
-    r.pbeg = g.pbeg;
-    r.pend = g.pend;
-    const int cap_dst = (l % 2 == 0) ? args.capB : args.capA;  // level l writes B if l even
-    const int zend = ZL + r.ncn + L + 2 * VR + 16;
-    r.zend = last ? 0 : (zend < cap_dst ? zend : cap_dst);
-    r.small = g.small;
-    r.pad = 0;
-    r.drow = args.details[l]
-                 ? static_cast<const S*>(args.details[l]) + row * (int64_t)r.nc
-                 : nullptr;
-    r.pad2[0] = r.pad2[1] = 0;
-    lrec[l] = r;
-  }
-
-  // Prefetch registers hold raw coefficients; the loads are issued here and range-masked and
-  // converted only when staged, so no wait follows a load where it is issued.
-  const int dspan = PR + H + 4;
-  constexpr int PFD = PR / NT + 1;  // dspan <= PFD * NT since H + 4 <= NT
-  S pf[PFD] = {};
-  auto fetch_d = [&](const S* dr, int ncl, int pbl) {
-    if (!dr) return;
+  // ---- prefetch registers: raw band values, converted only when staged
+  S pa[PA], pb[PB];
 #pragma unroll
-    for (int k = 0; k < PFD; ++k) {
-      // blocks of NT entirely outside the coefficients are skipped (block-uniform test)
-      if (k * NT < dspan && pbl + k * NT < ncl && pbl + k * NT + NT > 0)
-        pf[k] = dr[min(max(pbl + tid + k * NT, 0), ncl - 1)];
+  for (int k = 0; k < PA; ++k) pa[k] = S{};
+#pragma unroll
+  for (int k = 0; k < PB; ++k) pb[k] = S{};
+  // Descriptor tables are read once per row, in batches (an opaque zero offset keeps the
+  // compiler from hoisting all of them out of the row loop into scalar registers).
+  auto issue = [&](auto& regs, auto tab, int n, int64_t r, int z) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k0 = 0; k0 < n; k0 += 4) {
+      SynLoad d[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = tab[k0 + i + z];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (d[i].cnt > 0) {
+          const int e = tid < d[i].cnt ? tid : d[i].cnt - 1;
+          regs[k0 + i] = global_load(
+              reinterpret_cast<const S*>(static_cast<const char*>(d[i].base) + r * (int64_t)d[i].stride), e);
+        }
+      }
     }
   };
-  S pq[QR] = {};
+  auto stage = [&](auto& regs, auto tab, int n, uint32_t mask, int z) __attribute__((always_inline)) {
 #pragma unroll
-  for (int k = 0; k < QR; ++k) {
-    if (k < args.qslots && args.qs_ptr[k]) {
-      const int ncl = args.qs_nc[k];
-      const S* dr = static_cast<const S*>(args.qs_ptr[k]) + row * (int64_t)ncl;
-      pq[k] = dr[min(max(args.qs_u0[k] + tid, 0), ncl - 1)];
-    }
-  }
-  if (args.qlevels < levels) {
-    const int fl = args.qlevels;
-    const bool flast = fl + 1 == levels;
-    const int ncl = args.nc[fl];
-    const LevelGeom g =
-        level_geom(ncl, args.n_out[fl], flast ? 0 : args.nc[fl + 1], flast, L, off, mode);
-    const S* dr = args.details[fl] ? static_cast<const S*>(args.details[fl]) + row * (int64_t)ncl
-                                   : nullptr;
-    fetch_d(dr, ncl, g.ub0);
-  }
-
-  // the coarsest low band -> A, with zero margins; loads issued AB at a time
-  {
-    const int nc = args.nc[0];
-    const S* ag = args.approx ? static_cast<const S*>(args.approx) + row * (int64_t)nc : nullptr;
-    constexpr int AB = 9;
-    const int kend = min(args.capA, ZL + nc + L + 2 * VR + 16);
-    for (int k0 = tid; k0 < kend; k0 += AB * NT) {
-      S v[AB] = {};
-      if (ag) {
+    for (int k0 = 0; k0 < n; k0 += 8) {
+      uint32_t w[8];
 #pragma unroll
-        for (int j = 0; j < AB; ++j) v[j] = ag[min(max(k0 + j * NT - ZL, 0), nc - 1)];
-      }
+      for (int i = 0; i < 8; ++i) w[i] = k0 + i < n ? tab[k0 + i + z] : 0u;
 #pragma unroll
-      for (int j = 0; j < AB; ++j) {
-        const int k = k0 + j * NT;
-        const int u = k - ZL;
-        if (k < kend) A[k] = (ag && u >= 0 && u < nc) ? T(Storage<S>::load(v + j, 0)) : T(0);
+      for (int i = 0; i < 8; ++i) {
+        if (k0 + i < n && (mask & (1u << (k0 + i)))) {
+          const int dest = (int)(w[i] & 0x3ffffu), cnt = (int)(w[i] >> 18);
+          if (tid < cnt) lds[dest + tid] = T(Storage<S>::load(&regs[k0 + i], 0));
+        }
       }
     }
-  }
-  // the queued high bands -> D
+  };
+  auto issue_head = [&](int64_t r, int z) __attribute__((always_inline)) { issue(pa, args.ldA, PA, r, z); };
+  auto issue_tail = [&](int64_t r, int z) __attribute__((always_inline)) { issue(pb, args.ldB, PB, r, z); };
+  auto stage_head = [&](int l, int z) __attribute__((always_inline)) {
+    stage(pa, args.stA, PA, args.maskA[l], z);
+  };
+  auto stage_tail = [&](int z) __attribute__((always_inline)) { stage(pb, args.stB, PB, ~0u, z); };
+  auto wait_loads = [&]() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
+  // without prefetch: the bands of level l, NT * PB coefficients at a time through pb
+  auto direct = [&](int l, int64_t r) __attribute__((always_inline)) {
+    const int src = args.lv[l].src, dbuf = args.lv[l].dbuf;
+    for (int s = 0; s < 2; ++s) {
+      if (s == 0 && l > 0) continue;  // a_0 belongs to level 0 only
+      const S* band = static_cast<const S*>(args.band[s == 0 ? 0 : l + 1]);
+      if (!band) continue;
+      const int cnt = args.nc[l];
+      T* dstp = lds + (s == 0 ? src : dbuf) + ZL;
+      for (int c0 = 0; c0 < cnt; c0 += NT * PB) {
 #pragma unroll
-  for (int k = 0; k < QR; ++k) {
-    if (k < args.qslots && tid < args.qs_len[k]) {
-      const int u = args.qs_u0[k] + tid;
-      const bool ok = args.qs_ptr[k] && u >= 0 && u < args.qs_nc[k];
-      D[args.qs_pos[k] + tid] = ok ? T(Storage<S>::load(pq + k, 0)) : T(0);
-    }
-  }
-  __syncthreads();
-
-  T* src = A;
-  T* dst = B;
-  constexpr int BK = 3;  // band positions per band lane (at most 3 NT per level)
-  for (int l = 0; l < levels; ++l) {
-    const RLevel lr = load_rlevel(lrec + l);
-    const bool last = l + 1 == levels;
-    const int m = lr.m;
-    const int nc = lr.nc;
-    const T* a0 = src + ZL;  // a0[u] = low band coefficient u
-    S* orow = last ? static_cast<S*>(args.out) + row * (int64_t)m : nullptr;
-    const S* drow = static_cast<const S*>(lr.drow);
-
-    // zero the margins of the next low band (dst holds positions [0, mw) afterwards)
-    if (!last) {
-      for (int k = tid; k < ZL; k += NT) dst[k] = T(0);
-      for (int k = ZL + lr.ncn + tid; k < lr.zend; k += NT) dst[k] = T(0);
-    }
-
-    // 16-byte stores when provably aligned: off == 1 puts every thread's first position on a
-    // multiple of 4, and m % 4 == 0 keeps rows 16-byte aligned in global memory
-    const bool vec_out = std::is_same<S, float>::value && off == 1 && (m % 4) == 0;
-    const bool vec_lds = off == 1;
-    // other offsets put a thread's first position sh short of a 16-byte boundary: whole
-    // waves inside the plain range then store 16-byte blocks shifted by sh positions, taking
-    // the last sh values of each block from the next lane
-    const int sh = (4 - ((off - 1) & 3)) & 3;
-    const bool vec_shift = std::is_same<S, float>::value && last && sh != 0 && (m % 4) == 0;
-    T acc[BK];
-#pragma unroll
-    for (int j = 0; j < BK; ++j) acc[j] = T(0);
-    // band lane index of this thread (NT * BK: none).  With band <= 64 the left band runs
-    // on the top wave and the right band on the wave below it; otherwise band position b
-    // runs on lane NT - 1 - (b mod NT).
-    int bt = NT * BK;
-    {
-      const int wv = tid >> 6, ln = 63 - (tid & 63);
-      if (lr.band <= 64) {
-        if (wv == NT / 64 - 1) {
-          if (ln < lr.band) bt = ln;
-        } else if (wv == NT / 64 - 2) {
-          bt = lr.band + ln;
+        for (int k = 0; k < PB; ++k) {
+          const int c = c0 + k * NT + tid;
+          if (c0 + k * NT < cnt) pb[k] = global_load(band, r * (int64_t)cnt + (c < cnt ? c : cnt - 1));
         }
-      } else {
-        bt = NT - 1 - tid;
+        wait_loads();
+#pragma unroll
+        for (int k = 0; k < PB; ++k) {
+          const int c = c0 + k * NT + tid;
+          if (c < cnt) dstp[c] = T(Storage<S>::load(pb + k, 0));
+        }
       }
     }
+  };
+  auto zero = [&](int a, int b) __attribute__((always_inline)) {
+    for (int k = a + tid; k < b; k += NT) lds[k] = T(0);
+  };
 
-    for (int pi = 0; pi < lr.npass; ++pi) {
-      const int pb = lr.ub0 + pi * PR;
-      const T* dp;  // dp[u] = high band coefficient u (this pass's window)
-      if (lr.qoff >= 0) {
-        dp = D + lr.qoff - lr.ub0;
-      } else {
-        if (pi > 0) __syncthreads();  // the previous pass is done with D
+  const bool vec_lds = ((off - 1) & 3) == 0;  // a thread's first position is a multiple of 4
+  const int sh = (4 - ((off - 1) & 3)) & 3;    // else its distance to the next multiple of 4
+
+  // one level: margins, main pass, fold (the bands are staged)
+  // (always inlined: an outlined lambda would take the address of the kernel arguments, which
+  // then get copied to private memory)
+  auto level = [&](int l, int64_t row) __attribute__((always_inline)) {
+    const SynLevel lv = args.lv[l];
+    const bool last = l + 1 == J;
+    // zero margins of both bands (and the whole band when it is absent)
+    zero(lv.src, lv.src + ZL);
+    zero(lv.src + ZL + lv.nva, lv.src + ZL + lv.zhi);
+    zero(lv.dbuf, lv.dbuf + ZL);
+    zero(lv.dbuf + ZL + lv.nvd, lv.dbuf + ZL + lv.zhi);
+    __syncthreads();
+
+    // main pass
+    const int m = lv.m;
+    const T* a0 = lds + lv.src + ZL;   // a0[v] = low band coefficient v
+    const T* dp = lds + lv.dbuf + ZL;  // dp[v] = high band coefficient v
+    T* const E = lds + args.offE;
+    T* const dst = last ? nullptr : lds + lv.dst + ZL;
+    S* const orow = last ? static_cast<S*>(args.out) + row * (int64_t)m : nullptr;
+    const bool vec_out = std::is_same<S, float>::value && vec_lds && (m % 4) == 0;
+    const bool vec_shift = std::is_same<S, float>::value && sh != 0 && (m % 4) == 0;
+    const int plo = lv.plo, phi = lv.phi, pbeg = lv.pbeg, pend = lv.pend;
+    for (int vw = lv.vbeg + (tid - lane) * VR; vw < lv.vend; vw += NT * VR) {
+      const int v0 = vw + lane * VR;
+      if (v0 >= lv.vend) continue;
+      T zo[VR], ze[VR];
+      synthesis_block<T, LT, VR>(a0 + v0, dp + v0, h0, h1, L, zo, ze);
+      T v[2 * VR];
 #pragma unroll
-        for (int k = 0; k < PFD; ++k) {
-          const int idx = tid + k * NT;
-          const int u = pb + idx;
-          if (idx < dspan)
-            D[idx] = (drow && u >= 0 && u < nc) ? T(Storage<S>::load(pf + k, 0)) : T(0);
-        }
-        __syncthreads();
-        if (pi + 1 < lr.npass) {
-          fetch_d(drow, nc, pb + PR);
-        } else if (!last) {
-          const RLevel nr = load_rlevel(lrec + l + 1);
-          if (nr.qoff < 0) fetch_d(static_cast<const S*>(nr.drow), nr.nc, nr.ub0);
-        }
-        dp = D - pb;
+      for (int q = 0; q < VR; ++q) {
+        v[2 * q] = zo[q];
+        v[2 * q + 1] = ze[q];
       }
-
-      // main pass: positions [plo, phi)
-#pragma unroll
-      for (int g = 0; g < GR; ++g) {
-        const int lu = (g * NT + tid) * VR;  // coefficient offset inside the pass
-        const int ub = pb + lu;
-        const int i0 = 2 * ub + off - 1;     // first of this thread's 2 * VR positions
-        if (i0 + 2 * VR <= lr.plo || i0 >= lr.phi) continue;
-        T zo[VR], ze[VR];
-        synthesis_block<T, LT, VR>(a0 + ub, dp + ub, h0, h1, L, zo, ze);
-        T v[2 * VR];
-#pragma unroll
-        for (int q = 0; q < VR; ++q) {
-          v[2 * q] = zo[q];
-          v[2 * q + 1] = ze[q];
-        }
-        if constexpr (std::is_same<S, float>::value) {
-          const int iw = i0 - 2 * VR * (tid & 63);  // first position of the wave
-          if (vec_shift && iw >= lr.plo && iw + 128 * VR <= lr.phi) {
-            store_shifted(orow, i0, v, sh, tid & 63);
-            continue;
-          }
-        }
-        if (i0 >= lr.plo && i0 + 2 * VR <= lr.phi && (last ? vec_out : vec_lds)) {
-          typedef T v4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-          for (int q = 0; q < VR / 2; ++q) {
-            const v4 w = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-            if (last) {
-              if constexpr (std::is_same<S, float>::value)
-                *reinterpret_cast<v4*>(orow + i0 + 4 * q) = w;
-            } else {
-              *reinterpret_cast<v4*>(dst + ZL + i0 + 4 * q) = w;
-            }
-          }
+      const int i0 = 2 * v0 + off - 1;  // first of this thread's 2 VR positions
+      if constexpr (std::is_same<S, float>::value) {
+        // whole waves inside the plain range of the output row: shifted 16-byte stores
+        const int iw = 2 * vw + off - 1;
+        if (last && vec_shift && iw >= plo && iw + 128 * VR <= phi) {
+          store_shifted(orow, i0, v, sh, lane);
           continue;
         }
+      }
+      if (i0 >= plo && i0 + 2 * VR <= phi && (last ? vec_out : vec_lds)) {
+        typedef T v4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int j = 0; j < 2 * VR; ++j) {
-          const int i = i0 + j;
-          if (i >= lr.plo && i < lr.phi) {
-            if (last) Storage<S>::store(orow, i, v[j]);
-            else dst[ZL + i] = v[j];
+        for (int q = 0; q < VR / 2; ++q) {
+          const v4 w = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+          if (last) {
+            if constexpr (std::is_same<S, float>::value)
+              *reinterpret_cast<v4*>(orow + i0 + 4 * q) = w;
+          } else {
+            *reinterpret_cast<v4*>(dst + i0 + 4 * q) = w;
           }
         }
+        continue;
       }
-
-      // band lanes: the positions of this pass that fold onto band positions
-      if (bt < lr.nb) {
-        // the band lane index passes through an empty asm statement so that the compiler
-        // keeps this lane-specific set-up inside the branch (hoisted out of the pass loop it
-        // would run in every lane of every level)
-        int bo = bt;
-        asm volatile("" : "+v"(bo));
-        const int q0 = 2 * pb + off - 1;
-        const int lo = max(q0, lr.pbeg);
-        const int hi = min(q0 + 2 * PR, lr.pend);
 #pragma unroll
-        for (int j = 0; j < BK; ++j) {
-          const int b = bo + j * NT;
-          if (b < lr.nb) {
-            const int i = (lr.small || b < lr.band) ? b : m - 2 * lr.band + b;
-            acc[j] += band_sum<T, LT>(i, lo, hi, m, lr.md, lr.P, lr.pmin, lr.pmax, a0, dp, off,
-                                      h0, h1, L);
-          }
-        }
-      }
-    }
-    if (bt < lr.nb) {
-      int bo = bt;
-      asm volatile("" : "+v"(bo));
-#pragma unroll
-      for (int j = 0; j < BK; ++j) {
-        const int b = bo + j * NT;
-        if (b < lr.nb) {
-          const int i = (lr.small || b < lr.band) ? b : m - 2 * lr.band + b;
-          if (i < lr.mw) {
-            if (last) Storage<S>::store(orow, i, acc[j]);
-            else dst[ZL + i] = acc[j];
-          }
+      for (int j = 0; j < 2 * VR; ++j) {
+        const int p = i0 + j;
+        if (p >= plo && p < phi) {
+          if (last) Storage<S>::store(orow, p, v[j]);
+          else dst[p] = v[j];
+        } else if (p >= pbeg && p < pend) {
+          E[p < plo ? p - pbeg : (plo - pbeg) + (p - phi)] = v[j];
         }
       }
     }
     __syncthreads();
-    T* t = src;
-    src = dst;
-    dst = t;
+
+    // fold targets near the row ends (none in zero mode); the next level's staging (other
+    // LDS regions) may run meanwhile
+    const int nl = plo < lv.mw ? plo : lv.mw;
+    for (int t = tid; t < lv.nt; t += NT) {
+      const int i = t < nl ? t : phi + (t - nl);
+      const T s = fold_parked(E, i, m, lv.md, lv.P, pbeg, pend, plo, phi);
+      if (last) Storage<S>::store(orow, i, s);
+      else dst[i] = s;
+    }
+  };
+
+  // (one schedule for every row, with unconditional loads: a load issued on some paths only
+  // would make the compiler copy the prefetch registers between paths, and every copy of a
+  // register whose load is in flight waits for all loads)
+  int64_t row = blockIdx.x;
+  if constexpr (PRE) issue_head(row, 0);
+  for (; row < rows; row += gridDim.x) {
+    const int64_t next = row + gridDim.x < rows ? row + gridDim.x : rows - 1;
+    int z = 0;
+    asm volatile("" : "+s"(z));
+    if constexpr (PRE) {
+      // levels 0 .. J-2: the head (requested before the previous row's last level) is
+      // complete after this wait; this row's tail is requested here, waited for at level J-1
+      wait_loads();
+      stage_head(0, z);
+      issue_tail(row, z);
+    } else {
+      direct(0, row);
+    }
+    for (int l = 0; l + 1 < J; ++l) {
+      if (l > 0) {
+        if constexpr (PRE) stage_head(l, z);
+        else direct(l, row);
+      }
+      level(l, row);
+    }
+    // level J-1: the tail; the next row's head is requested before the main pass, whose
+    // duration covers its latency
+    if constexpr (PRE) {
+      wait_loads();
+      stage_tail(z);
+      issue_head(next, z);
+    } else if (J > 1) {
+      direct(J - 1, row);
+    }
+    level(J - 1, row);
   }
 }
 
@@ -1329,12 +1334,45 @@ int launch_schain(const SChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
   return 0;
 }
 
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Workgroups of a persistent whole-row kernel: as many as fit on the device at once (by its
+// occupancy at this LDS size), then evened out so that every workgroup gets the same number
+// of rows (the last one possibly fewer).
+template <typename K>
+inline int64_t persistent_grid(K kernel, size_t lds, int64_t rows) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                   NT, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int64_t full = (int64_t)per_cu * device_cus();
+  if (rows <= full) return rows;
+  const int64_t per_wg = cdiv(rows, full);
+  return cdiv(rows, per_wg);
+}
+
 template <typename S, typename T, int LT>
-int launch_rchain(const RChainArgs& a, int64_t rows, size_t lds, hipStream_t st) {
-  auto k = synthesis_rows_kernel<S, T, LT>;
-  static const bool lds_ok = allow_full_lds(k);
+int launch_rchain(const SynArgs& a, size_t lds, hipStream_t st) {
+  static const bool lds_ok = allow_full_lds(synthesis_rows_kernel<S, T, LT, true>) &&
+                             allow_full_lds(synthesis_rows_kernel<S, T, LT, false>);
   (void)lds_ok;
-  hipLaunchKernelGGL(k, dim3((unsigned)rows), dim3(NT), lds, st, a);
+  auto k = a.prefetch ? synthesis_rows_kernel<S, T, LT, true> : synthesis_rows_kernel<S, T, LT, false>;
+  const int64_t grid = persistent_grid(k, lds, a.rows);
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(NT), lds, st, a);
   FDWT_CHECK_LAUNCH();
   return 0;
 }
@@ -1375,18 +1413,18 @@ int run_schain(const SChainArgs& a, int64_t rows, int wg, size_t lds, hipStream_
 }
 
 template <typename S>
-int run_rchain(const RChainArgs& a, int64_t rows, size_t lds, hipStream_t st, bool templated) {
-  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_rchain, a, rows, lds, st) }
-  return launch_rchain<S, float, 0>(a, rows, lds, st);
+int run_rchain(const SynArgs& a, size_t lds, hipStream_t st, bool templated) {
+  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_rchain, a, lds, st) }
+  return launch_rchain<S, float, 0>(a, lds, st);
 }
 
-int dispatch_rchain(const RChainArgs& a, int64_t rows, size_t lds, int dtype, hipStream_t st) {
+int dispatch_rchain(const SynArgs& a, size_t lds, int dtype, hipStream_t st) {
   const bool templ = a.taps <= MAXL_T;
   switch (dtype) {
-    case FDWT_F32: return run_rchain<float>(a, rows, lds, st, templ);
-    case FDWT_F16: return run_rchain<__half>(a, rows, lds, st, templ);
-    case FDWT_BF16: return run_rchain<bf16_t>(a, rows, lds, st, templ);
-    case FDWT_F64: return launch_rchain<double, double, 0>(a, rows, lds, st);
+    case FDWT_F32: return run_rchain<float>(a, lds, st, templ);
+    case FDWT_F16: return run_rchain<__half>(a, lds, st, templ);
+    case FDWT_BF16: return run_rchain<bf16_t>(a, lds, st, templ);
+    case FDWT_F64: return launch_rchain<double, double, 0>(a, lds, st);
     default: return FDWT_ERR_ARG;
   }
 }
@@ -1478,13 +1516,10 @@ extern "C" int64_t fdwt_chain_max_length(int32_t taps, int32_t dtype) {
   int64_t n = 2 * (budget - stage - 6 * (int64_t)taps);
   const int64_t n2 = (budget - 6 * (int64_t)taps) * 4 / 3;
   if (n2 / 4 > stage) n = n2;  // the n/4 term dominates the staging window
-  // synthesis (whole-row kernel): level table + outputs n/2 and n/4 with margins + the pass
-  // window D + taps
-  const int64_t zl = (taps + 3) & ~3;
-  const int64_t margin = zl + taps + 2 * VR + 24 + 4;
-  const int64_t sbudget = (160 * 1024 - RLEVEL_BYTES) / compute_size(dtype) - 2 * margin -
-                          (PR + taps / 2 + 12) - 2 * (int64_t)taps - 8;
-  const int64_t ns = sbudget * 4 / 3 - 8;
+  // synthesis (whole-row kernel): tables (< 8 KiB) + P ~ n/2, Q + D ~ n/2 (the last level's
+  // two bands), each with margins of about 2L + 16, the parked fold values (< 4L + 8) and the
+  // taps: n + 12 L + 80 elements at most
+  const int64_t ns = (160 * 1024 - 8192) / compute_size(dtype) - 12 * (int64_t)taps - 96;
   if (ns < n) n = ns;
   return n > 0 ? n : 0;
 }
@@ -1542,70 +1577,89 @@ extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* ap
   return dispatch_achain(a, rows, wg, lds, dtype, static_cast<hipStream_t>(stream));
 }
 
-// Whole-row synthesis chain: LDS layout, queue placement and launch.
+// Whole-row synthesis chain: LDS layout, level records and prefetch jobs, launch.
+// Returns FDWT_ERR_TOO_LONG when a row does not fit in 160 KiB of LDS.
 int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st) {
-  RChainArgs a{};
-  const int levels = s.levels, L = s.taps, off = s.off, mode = s.mode;
-  a.approx = s.approx;
+  const int J = s.levels, L = s.taps;
+  if (J > FDWT_SYN_MAX_LEVELS) return FDWT_ERR_ARG;
+  const int ZL = (L + 3) & ~3;
+  const int cs = compute_size(dtype);
+  SynGeom geo[FDWT_SYN_MAX_LEVELS];
+  int64_t capP = 0, capQ = 0, capD = 0, capE = 4;
+  int64_t need_last = 0;
+  for (int l = 0; l < J; ++l) {
+    const bool last = l + 1 == J;
+    geo[l] = syn_geom(s.nc[l], s.n_out[l], last ? 0 : s.nc[l + 1], last, L, s.off, s.mode);
+    const int64_t need = ZL + (int64_t)geo[l].zhi;  // coefficients -ZL .. zhi of either band
+    if (((J - 1 - l) & 1) == 0) capP = std::max(capP, need);
+    else capQ = std::max(capQ, need);
+    if (last) need_last = need;
+    else capD = std::max(capD, need);
+    capE = std::max<int64_t>(capE, geo[l].ne);
+  }
+  capD = std::max(capD, need_last - capQ);  // the last level's high band spans Q and D
+  auto r4 = [](int64_t v) { return (v + 3) & ~(int64_t)3; };
+  const int64_t yP = 0, yQ = r4(capP), yD = yQ + r4(capQ), yE = yD + r4(capD);
+  const int64_t yT = yE + r4(capE);
+  const size_t lds = (size_t)(yT + r4(2 * L)) * cs;
+  if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
+
+  SynArgs a{};
+  a.band[0] = s.approx;
+  for (int l = 0; l < J; ++l) {
+    a.band[l + 1] = s.details[l];
+    a.nc[l] = s.nc[l];
+    const SynGeom& g = geo[l];
+    SynLevel& r = a.lv[l];
+    r.m = g.m;
+    r.mw = g.mw;
+    r.md = g.md;
+    r.P = g.P;
+    r.pbeg = g.pbeg;
+    r.pend = g.pend;
+    r.plo = g.plo;
+    r.phi = g.phi;
+    r.vbeg = g.vbeg;
+    r.vend = g.vend;
+    r.zhi = g.zhi;
+    r.nt = g.nt;
+    r.src = syn_src(l, J, (int)yP, (int)yQ);
+    r.dst = l + 1 == J ? -1 : syn_src(l + 1, J, (int)yP, (int)yQ);
+    r.dbuf = syn_dbuf(l, J, (int)yQ, (int)yD);
+    r.nva = l > 0 ? s.nc[l] : (s.approx ? s.nc[0] : 0);
+    r.nvd = s.details[l] ? s.nc[l] : 0;
+  }
+  const bool pre = syn_regs(
+      J, s.nc, s.approx, s.details, ZL, (int)yP, (int)yQ, (int)yD,
+      [&](bool tail, int k, int c0, int cnt, int dest, int l, bool is_approx) {
+        const void* band = is_approx ? s.approx : s.details[l];
+        const int es = dtype_size(dtype);
+        const SynLoad ld{static_cast<const char*>(band) + (size_t)c0 * es, s.nc[l] * es, cnt};
+        if (tail) {
+          a.ldB[k] = ld;
+          a.stB[k] = syn_stage_word(dest, cnt);
+        } else {
+          a.ldA[k] = ld;
+          a.stA[k] = syn_stage_word(dest, cnt);
+          a.maskA[l] |= 1u << k;
+        }
+      });
+  if (!pre) {  // no prefetch: clear whatever was filled before the overflow
+    for (int k = 0; k < PA; ++k) a.ldA[k] = SynLoad{nullptr, 0, 0}, a.stA[k] = 0;
+    for (int k = 0; k < PB; ++k) a.ldB[k] = SynLoad{nullptr, 0, 0}, a.stB[k] = 0;
+    for (int l = 0; l < J; ++l) a.maskA[l] = 0;
+  }
   a.out = s.out;
   a.h0 = s.h0;
   a.h1 = s.h1;
-  a.levels = levels;
+  a.rows = rows;
+  a.levels = J;
   a.taps = L;
-  a.mode = mode;
-  a.off = off;
-  const int64_t zl = (L + 3) & ~3;
-  const int64_t margin = zl + L + 2 * VR + 24;
-  int64_t capA = s.nc[0] + margin, capB = 4;
-  const int64_t capD = (PR + L / 2 + 8 + 3) & ~3;
-  int slot = 0;
-  int64_t qpos = 0;
-  bool queue_open = true;
-  for (int l = 0; l < levels; ++l) {
-    const bool last = l + 1 == levels;
-    a.details[l] = s.details[l];
-    a.nc[l] = s.nc[l];
-    a.n_out[l] = s.n_out[l];
-    a.qoff[l] = -1;
-    const LevelGeom g = level_geom(s.nc[l], s.n_out[l], last ? 0 : s.nc[l + 1], last, L, off, mode);
-    if (g.nb > 3 * NT) return FDWT_ERR_TOO_LONG;
-    if (!last) {
-      const int64_t need = s.n_out[l] + margin;  // output of level l = low band of level l + 1
-      if (l % 2 == 0) capB = std::max(capB, need);
-      else capA = std::max(capA, need);
-    }
-    // the queue takes a prefix of the levels (never the last), each a single pass
-    if (queue_open && !last) {
-      const int64_t ub_last = (g.pend - off) >> 1;
-      const int64_t len = ub_last - g.ub0 + 2 * VR + L / 2 + 4;
-      const int ns = (int)cdiv(len, NT);
-      if (g.npass != 1 || slot + ns > QR || qpos + len > capD) {
-        queue_open = false;
-      } else {
-        a.qoff[l] = (int32_t)qpos;
-        for (int k = 0; k < ns; ++k, ++slot) {
-          a.qs_ptr[slot] = s.details[l];
-          a.qs_nc[slot] = s.nc[l];
-          a.qs_u0[slot] = (int32_t)(g.ub0 + (int64_t)k * NT);
-          a.qs_pos[slot] = (int32_t)(qpos + (int64_t)k * NT);
-          a.qs_len[slot] = (int32_t)std::min<int64_t>(NT, len - (int64_t)k * NT);
-        }
-        qpos = (qpos + len + 3) & ~(int64_t)3;
-        a.qlevels = l + 1;
-      }
-    } else {
-      queue_open = false;
-    }
-  }
-  a.qslots = slot;
-  a.capA = (int)((capA + 3) & ~3);
-  a.capB = (int)((capB + 3) & ~3);
-  a.capD = (int)capD;
-  const size_t lds = (size_t)RLEVEL_BYTES +
-                     (size_t)(a.capA + a.capB + a.capD + 2 * L + 4) * compute_size(dtype);
-  if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
-  if (rows > INT32_MAX) return FDWT_ERR_ARG;
-  return dispatch_rchain(a, rows, lds, dtype, st);
+  a.off = s.off;
+  a.prefetch = pre ? 1 : 0;
+  a.offE = (int32_t)yE;
+  a.offTap = (int32_t)yT;
+  return dispatch_rchain(a, lds, dtype, st);
 }
 
 extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* details, void* out,

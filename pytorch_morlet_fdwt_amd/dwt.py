@@ -27,6 +27,7 @@ __all__ = ["dwt", "idwt", "wavedec", "waverec", "dwt_max_level", "dwt_coeff_len"
 
 MODES = {"zero": 0, "periodic": 1, "symmetric": 2, "reflect": 3, "periodization": 4}
 _PERIODIZATION = MODES["periodization"]
+_SYN_MAX_LEVELS = 16  # FDWT_SYN_MAX_LEVELS: levels per fdwt_synthesis_chain launch
 _ZERO = MODES["zero"]
 
 
@@ -110,13 +111,17 @@ def _synthesis_chain(a2, ds, h0, h1, mode, off, nc, n_out, R, dtype, device):
     while k_end > 1 and not _chain_fits(n_out[k_end - 1], taps, dtype):
         k_end -= 1
     cur = None
-    if k_end >= 1:
-        cur = torch.empty((R, n_out[k_end - 1]), device=device, dtype=dtype)
+    # at most _SYN_MAX_LEVELS levels per launch; a later group starts from the first nc[g0]
+    # samples of the previous group's output
+    for g0 in range(0, k_end, _SYN_MAX_LEVELS):
+        g1 = min(k_end, g0 + _SYN_MAX_LEVELS)
+        a_in = a2 if g0 == 0 else cur[:, :nc[g0]].contiguous()
+        cur = torch.empty((R, n_out[g1 - 1]), device=device, dtype=dtype)
         if R:
             _lib.launch("fdwt_synthesis_chain", device,
-                        _lib.ptr(a2), _lib.ptr_array(ds[:k_end]), _lib.ptr(cur), _lib.ptr(h0),
-                        _lib.ptr(h1), R, _lib.i64_array(nc[:k_end]),
-                        _lib.i64_array(n_out[:k_end]), k_end, taps, mode, off,
+                        _lib.ptr(a_in), _lib.ptr_array(ds[g0:g1]), _lib.ptr(cur), _lib.ptr(h0),
+                        _lib.ptr(h1), R, _lib.i64_array(nc[g0:g1]),
+                        _lib.i64_array(n_out[g0:g1]), g1 - g0, taps, mode, off,
                         _lib.dtype_code(dtype), _lib.stream(device))
     for k in range(k_end, K):
         a = cur[:, :nc[k]].contiguous()

@@ -141,6 +141,28 @@ def test_fused_backward_matches_oracle(mode):
 
 
 @pytest.mark.parametrize("mode", MODES)
+def test_chains_deeper_than_one_launch(mode):
+    """More levels than one synthesis launch takes (FDWT_SYN_MAX_LEVELS = 16): lengths
+    saturate at a few coefficients, as with pywt when level exceeds dwt_max_level."""
+    for wavelet, n, level in (("haar", 100, 20), ("db2", 37, 18)):
+        x = _rand((3, n), 5)
+        xg = x.to(DEV).requires_grad_()
+        xc = x.clone().requires_grad_()
+        cg = fdwt.wavedec(xg, wavelet, mode, level)
+        cc = O.wavedec(xc, wavelet, mode, level)
+        for g, c in zip(cg, cc):
+            torch.testing.assert_close(g.detach().cpu(), c.detach(), atol=1e-12, rtol=1e-12)
+        wts = [_rand(c.shape, 31 + i) for i, c in enumerate(cc)]
+        yg = fdwt.waverec([c * w.to(DEV) for c, w in zip(cg, wts)], wavelet, mode)
+        yc = O.waverec([c * w for c, w in zip(cc, wts)], wavelet, mode)
+        torch.testing.assert_close(yg.detach().cpu(), yc.detach(), atol=1e-12, rtol=1e-12)
+        gy = _rand(yc.shape, 41)
+        (yg * gy.to(DEV)).sum().backward()
+        (yc * gy).sum().backward()
+        torch.testing.assert_close(xg.grad.cpu(), xc.grad, atol=1e-11, rtol=1e-11)
+
+
+@pytest.mark.parametrize("mode", MODES)
 def test_gradcheck_and_gradgradcheck(mode):
     """tests/test_dwt.py:58-72 of the reference, on the HIP kernels in float64."""
     for wavelet in ["haar", "db3", "bior3.5"]:
