@@ -196,60 +196,160 @@ __global__ void __launch_bounds__(NT) morlet_backward_x_kernel(Stage st, const T
 
 // ------------------------------------------------------------------ filter gradient
 // Partial sums per workgroup of  gh[s][k][ch] = sum_n g[s, n, ch] x[n + x_off - dil (k - half)]
-// for k = 0 .. 2 half (every tap, no symmetry assumed).  Lane i of a wave handles positions
-// i, i + 64, ... of the tile (conflict-free LDS reads), KB taps at a time sharing each g
-// load; the 64 lanes are then summed with wave shuffles.  partial: (n_el, blocks) with
+// for k = 0 .. 2 half (every tap, no symmetry assumed).  partial: (n_el, blocks) with
 // n_el = n_scales (2 half + 1) C, written transposed so that the final reduction reads
 // contiguous memory.
-constexpr int KB = 8;
+//
+// Register tiling: g of up to HS scales is staged in LDS next to the x tile; each wave takes
+// blocks of HB taps, and each lane HP consecutive positions at a time, so one 16-byte LDS read
+// of x feeds HP positions x C channels x HS scales FMAs (for dil <= 2 the taps of a block
+// share one window of x, read once).  Lane l handles positions HP l + 64 HP q; at the end the
+// HS HB C sums of a lane are reduced over the 64 lanes of the wave by a butterfly that halves
+// the values per lane at every step (reduce-scatter), then written by the lanes that hold them.
+constexpr int HB = 8;   // taps per block
+constexpr int HS = 4;   // scales per group
+constexpr int HP = 4;   // consecutive positions per lane and step
+constexpr int HPAD = 16;  // zeros in front of the x tile (window reads of clamped taps)
 
-template <typename T, bool CPLX>
+// One step of butterfly_sum: with offset O and W values per lane, a lane keeps the half of
+// its values selected by (lane & O), summed with its partner's copy of that half.
+template <typename T, int O, int W>
+__device__ inline void butterfly_step(T (&v)[64], int lane) {
+  if constexpr (O > 0) {
+    if constexpr (W > 1) {
+      const bool hi = lane & O;
+#pragma unroll
+      for (int j = 0; j < W / 2; ++j) {
+        const T send = hi ? v[j] : v[j + W / 2];
+        const T keep = hi ? v[j + W / 2] : v[j];
+        v[j] = keep + __shfl_xor(send, O);
+      }
+      butterfly_step<T, O / 2, W / 2>(v, lane);
+    } else {
+      v[0] += __shfl_xor(v[0], O);
+      butterfly_step<T, O / 2, 1>(v, lane);
+    }
+  }
+}
+
+// Sum W values per lane over the 64 lanes of a wave, leaving one sum per lane (v[0]).
+template <typename T, int W>
+__device__ inline void butterfly_sum(T (&v)[64], int lane) {
+  butterfly_step<T, 32, W>(v, lane);
+}
+
+// Index of the value a lane holds after butterfly_sum over W values: the bits of the lane
+// picked by the halving steps (offsets 32, 16, ..) read from the most significant side.
+template <int W>
+__device__ inline int butterfly_index(int lane) {
+  int idx = 0;
+#pragma unroll
+  for (int o = 32, w = W; o > 0 && w > 1; o >>= 1, w >>= 1) idx = 2 * idx + ((lane & o) ? 1 : 0);
+  return idx;
+}
+
+template <typename T, bool CPLX, int DIL>  // DIL: 1, 2, or 0 for any multiple of 4
 __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T* __restrict__ g,
                                                                T* __restrict__ partial,
                                                                int g_scales, int tiles) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int C = CPLX ? 2 : 1;
-  T* X = reinterpret_cast<T*>(smem_raw);
-  const int half = st.half, dil = st.dil;
+  constexpr int NV = HS * HB * C;  // sums per lane (a power of two)
+  static_assert((NV & (NV - 1)) == 0 && NV <= 64, "butterfly needs a power of two <= 64");
+  T* const X = reinterpret_cast<T*>(smem_raw) + HPAD;  // X[-HPAD..-1] = 0
+  const int half = st.half, dil = DIL > 0 ? DIL : st.dil;
   const int span = TT + 2 * dil * half;
-  T* G = X + ((span + 3) & ~3);  // one scale of g, de-interleaved: G[ch * TT + i]
+  T* const G = X + ((span + 4 + 3) & ~3);  // G[(sl C + ch) TT + i], HS scales
   const int64_t row = blockIdx.x / tiles;
   const int64_t n0 = (int64_t)(blockIdx.x % tiles) * TT;
   const int64_t nblocks = (int64_t)gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const T* xrow = static_cast<const T*>(st.x) + row * st.n_in;
-  stage_row(X, xrow, n0 + st.x_off - (int64_t)dil * half, span, st.n_in);
+  if (tid < HPAD) X[tid - HPAD] = T(0);
+  stage_row(X, xrow, n0 + st.x_off - (int64_t)dil * half, span + 4, st.n_in);
   const int K = 2 * half + 1;
   const int nvalid = (int)min((int64_t)TT, st.n_out - n0);
-  for (int s = 0; s < st.n_scales; ++s) {
-    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out + n0) * C;
+  typedef T v4 __attribute__((ext_vector_type(4)));
+  for (int s0 = 0; s0 < st.n_scales; s0 += HS) {
+    const int ns = min(HS, st.n_scales - s0);
     __syncthreads();
-    for (int k = tid; k < TT * C; k += NT) {
-      const int i = k / C, ch = k % C;
-      G[ch * TT + i] = (i < nvalid) ? grow[k] : T(0);
+    for (int k = tid; k < HS * TT * C; k += NT) {
+      const int sl = k / (TT * C), r = k % (TT * C), i = r / C, ch = r % C;
+      T v = T(0);
+      if (sl < ns && i < nvalid)
+        v = g[((row * g_scales + st.chan[s0 + sl]) * st.n_out + n0) * C + r];
+      G[(sl * C + ch) * TT + i] = v;
     }
     __syncthreads();
-    for (int k0 = wave * KB; k0 < K; k0 += (NT / 64) * KB) {
+    for (int k0 = wave * HB; k0 < K; k0 += (NT / 64) * HB) {
+      T acc[HS][HB][C];
 #pragma unroll
-      for (int ch = 0; ch < C; ++ch) {
-        T acc[KB];
+      for (int a = 0; a < HS; ++a)
 #pragma unroll
-        for (int b = 0; b < KB; ++b) acc[b] = T(0);
-        for (int i = lane; i < nvalid; i += 64) {
-          const T gv = G[ch * TT + i];
+        for (int b = 0; b < HB; ++b)
 #pragma unroll
-          for (int b = 0; b < KB; ++b) {
-            const int k = min(k0 + b, K - 1);  // X index of position i is i + dil (2 half - k)
-            acc[b] = fma(gv, X[i + dil * (2 * half - k)], acc[b]);
+          for (int ch = 0; ch < C; ++ch) acc[a][b][ch] = T(0);
+      for (int q = 0; q < TT / (64 * HP); ++q) {
+        const int i = (q * 64 + lane) * HP;
+        T gv[HS][C][HP];
+#pragma unroll
+        for (int a = 0; a < HS; ++a)
+#pragma unroll
+          for (int ch = 0; ch < C; ++ch) {
+            const v4 w = *reinterpret_cast<const v4*>(G + (a * C + ch) * TT + i);
+#pragma unroll
+            for (int p = 0; p < HP; ++p) gv[a][ch][p] = w[p];
+          }
+        if constexpr (DIL > 0) {
+          // taps k0 .. k0 + HB - 1 read x[i + p + DIL (2 half - k)]: one window of
+          // HP + DIL (HB - 1) values starting at i + DIL (2 half - k0 - HB + 1)
+          constexpr int NW = HP + DIL * (HB - 1);
+          const T* xw = X + i + DIL * (2 * half - k0 - (HB - 1));
+          T wv[NW];
+#pragma unroll
+          for (int m = 0; m < NW; ++m) wv[m] = xw[m];
+#pragma unroll
+          for (int b = 0; b < HB; ++b)
+#pragma unroll
+            for (int p = 0; p < HP; ++p) {
+              const T xv = wv[p + DIL * (HB - 1 - b)];
+#pragma unroll
+              for (int a = 0; a < HS; ++a)
+#pragma unroll
+                for (int ch = 0; ch < C; ++ch) acc[a][b][ch] = fma(gv[a][ch][p], xv, acc[a][b][ch]);
+            }
+        } else {
+#pragma unroll
+          for (int b = 0; b < HB; ++b) {
+            const int k = min(k0 + b, K - 1);
+            const v4 w = *reinterpret_cast<const v4*>(X + i + dil * (2 * half - k));
+#pragma unroll
+            for (int p = 0; p < HP; ++p)
+#pragma unroll
+              for (int a = 0; a < HS; ++a)
+#pragma unroll
+                for (int ch = 0; ch < C; ++ch) acc[a][b][ch] = fma(gv[a][ch][p], w[p], acc[a][b][ch]);
           }
         }
+      }
+      // positions beyond nvalid have g = 0 and add nothing
+      T v[64];
 #pragma unroll
-        for (int b = 0; b < KB; ++b) {
-          T v = acc[b];
-          for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-          if (lane == 0 && k0 + b < K)
-            partial[((int64_t)(s * K + k0 + b) * C + ch) * nblocks + blockIdx.x] = v;
-        }
+      for (int a = 0; a < HS; ++a)
+#pragma unroll
+        for (int b = 0; b < HB; ++b)
+#pragma unroll
+          for (int ch = 0; ch < C; ++ch) v[(a * HB + b) * C + ch] = acc[a][b][ch];
+      butterfly_sum<T, NV>(v, lane);
+      // the lanes holding value j: lane bits picked by the halving steps; with NV < 64 the
+      // remaining steps left several lanes with the same sum, and the first of them writes
+      const int j = butterfly_index<NV>(lane);
+      const int rest = 64 / NV;  // lanes sharing one sum: those differing in the low bits
+      if ((lane & (rest - 1)) == 0) {
+        const int a = j / (HB * C), b = (j / C) % HB, ch = j % C;
+        const int k = k0 + b;
+        if (a < ns && k < K)
+          partial[((int64_t)((s0 + a) * K + k) * C + ch) * nblocks + blockIdx.x] = v[0];
       }
     }
   }
@@ -766,16 +866,23 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
   const int64_t span = TT + 2 * (int64_t)dil * half;
-  const size_t lds = (size_t)(((span + 3) & ~3) + TT * channels) * cs;
+  const size_t lds = (size_t)(HPAD + ((span + 4 + 3) & ~3) + (int64_t)HS * TT * channels) * cs;
   const int64_t blocks = rows * tiles;
   if (n_el > INT32_MAX) return FDWT_ERR_ARG;
+  if (dil != 1 && dil != 2 && dil % 4 != 0) return FDWT_ERR_ARG;
   int rc;
-#define BWH(TYPE, CPLX)                                                                       \
+#define BWH_DIL(TYPE, CPLX, D)                                                                \
   do {                                                                                        \
-    auto k = morlet_backward_h_kernel<TYPE, CPLX>;                                            \
+    auto k = morlet_backward_h_kernel<TYPE, CPLX, D>;                                         \
     FDWT_LDS_ONCE(k);                                                                         \
     rc = launch(k, blocks, lds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,      \
                 tiles);                                                                       \
+  } while (0)
+#define BWH(TYPE, CPLX)                                                                       \
+  do {                                                                                        \
+    if (dil == 1) BWH_DIL(TYPE, CPLX, 1);                                                     \
+    else if (dil == 2) BWH_DIL(TYPE, CPLX, 2);                                                \
+    else BWH_DIL(TYPE, CPLX, 0);                                                              \
     if (rc) return rc;                                                                        \
     return launch(reduce_cols_kernel<TYPE>, n_el, 0, hs, (const TYPE*)workspace, (TYPE*)gh,   \
                   blocks, (int)accumulate);                                                   \
@@ -787,6 +894,7 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   if (channels == 2) BWH(double, true);
   BWH(double, false);
 #undef BWH
+#undef BWH_DIL
 }
 
 extern "C" int64_t fdwt_mix_workspace(int64_t rows, int64_t n_out, int32_t n_scales) {
