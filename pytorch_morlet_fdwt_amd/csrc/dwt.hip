@@ -181,9 +181,20 @@ __host__ __device__ inline uint32_t syn_stage_word(int dest, int cnt) {
   return (uint32_t)dest | ((uint32_t)cnt << 18);
 }
 
-// Arguments of the whole-row synthesis kernel.  Every table the kernel reads per level or per
-// register lives here, so it reaches the kernel through scalar loads of the kernel arguments
-// (no vector instruction spent on it).
+// Tables of the whole-row synthesis kernel, passed in the kernel arguments and copied to LDS
+// by each workgroup once: the kernel reads them at every level and row, and LDS reads (a
+// broadcast address) are far cheaper than scalar loads of the argument segment.
+struct SynTab {
+  uint32_t maskA[FDWT_SYN_MAX_LEVELS];  // head registers staged at each level
+  SynLevel lv[FDWT_SYN_MAX_LEVELS];
+  SynLoad ldA[PA];  // head registers
+  SynLoad ldB[PB];  // tail registers
+  uint32_t stA[PA];
+  uint32_t stB[PB];
+};
+static_assert(sizeof(SynTab) % 16 == 0, "the LDS copy uses whole 16-byte words");
+
+// Arguments of the whole-row synthesis kernel.
 struct SynArgs {
   // band[0] = the coarsest approximation, band[l + 1] = the details of level l (one array: a
   // run-time choice between two argument fields would make the compiler copy the arguments to
@@ -196,12 +207,7 @@ struct SynArgs {
   int32_t nc[FDWT_SYN_MAX_LEVELS];
   int32_t levels, taps, off, prefetch;  // prefetch: the bands fit the head and tail registers
   int32_t offE, offTap;
-  uint32_t maskA[FDWT_SYN_MAX_LEVELS];  // head registers staged at each level
-  SynLevel lv[FDWT_SYN_MAX_LEVELS];
-  SynLoad ldA[PA];  // head registers
-  SynLoad ldB[PB];  // tail registers
-  uint32_t stA[PA];
-  uint32_t stB[PB];
+  SynTab tab;
 };
 
 // The prefetch registers of a row: each band of the head (a_0, d_0 .. d_{J-2} when J > 1)
@@ -1070,7 +1076,8 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
 #else
   const SynArgs& args = *static_cast<const SynArgs*>(nullptr);
 #endif
-  T* const lds = reinterpret_cast<T*>(smem_raw);
+  SynTab* const tab = reinterpret_cast<SynTab*>(smem_raw);
+  T* const lds = reinterpret_cast<T*>(smem_raw + sizeof(SynTab));
   const int J = args.levels;
   const int L = LT > 0 ? LT : args.taps;
   const int ZL = (L + 3) & ~3;
@@ -1096,8 +1103,19 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
     load_taps(gh0, gh1, lds + args.offTap, lds + args.offTap + L, L, false);
     h0 = lds + args.offTap;
     h1 = lds + args.offTap + L;
-    __syncthreads();
   }
+  {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef __attribute__((address_space(4))) const v4i KWord;
+#else
+    typedef const v4i KWord;
+#endif
+    KWord* src = reinterpret_cast<KWord*>(&args.tab);
+    v4i* dst = reinterpret_cast<v4i*>(tab);
+    for (int k = tid; k < (int)(sizeof(SynTab) / 16); k += NT) dst[k] = src[k];
+  }
+  __syncthreads();
 
   // ---- prefetch registers: raw band values, converted only when staged
   S pa[PA], pb[PB];
@@ -1105,49 +1123,48 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
   for (int k = 0; k < PA; ++k) pa[k] = S{};
 #pragma unroll
   for (int k = 0; k < PB; ++k) pb[k] = S{};
-  // Descriptor tables are read once per row, in batches (an opaque zero offset keeps the
-  // compiler from hoisting all of them out of the row loop into scalar registers).
-  auto issue = [&](auto& regs, auto tab, int n, int64_t r, int z) __attribute__((always_inline)) {
+  // Load descriptors and staging words come from the LDS copy of the tables (every lane reads
+  // the same address); only a register's count needs to be wave-uniform (it guards the load).
+  auto issue = [&](auto& regs, const SynLoad* t, int n, int64_t r) __attribute__((always_inline)) {
 #pragma unroll
     for (int k0 = 0; k0 < n; k0 += 4) {
       SynLoad d[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = tab[k0 + i + z];
+      for (int i = 0; i < 4; ++i) d[i] = t[k0 + i];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (d[i].cnt > 0) {
-          const int e = tid < d[i].cnt ? tid : d[i].cnt - 1;
+        const int cnt = __builtin_amdgcn_readfirstlane(d[i].cnt);
+        if (cnt > 0) {
+          const int e = tid < cnt ? tid : cnt - 1;
           regs[k0 + i] = global_load(
               reinterpret_cast<const S*>(static_cast<const char*>(d[i].base) + r * (int64_t)d[i].stride), e);
         }
       }
     }
   };
-  auto stage = [&](auto& regs, auto tab, int n, uint32_t mask, int z) __attribute__((always_inline)) {
+  auto stage = [&](auto& regs, const uint32_t* t, int n, uint32_t mask) __attribute__((always_inline)) {
 #pragma unroll
-    for (int k0 = 0; k0 < n; k0 += 8) {
-      uint32_t w[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) w[i] = k0 + i < n ? tab[k0 + i + z] : 0u;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (k0 + i < n && (mask & (1u << (k0 + i)))) {
-          const int dest = (int)(w[i] & 0x3ffffu), cnt = (int)(w[i] >> 18);
-          if (tid < cnt) lds[dest + tid] = T(Storage<S>::load(&regs[k0 + i], 0));
-        }
+    for (int k = 0; k < n; ++k) {
+      if (mask & (1u << k)) {
+        const uint32_t w = t[k];
+        const int dest = (int)(w & 0x3ffffu), cnt = (int)(w >> 18);
+        if (tid < cnt) lds[dest + tid] = T(Storage<S>::load(&regs[k], 0));
       }
     }
   };
-  auto issue_head = [&](int64_t r, int z) __attribute__((always_inline)) { issue(pa, args.ldA, PA, r, z); };
-  auto issue_tail = [&](int64_t r, int z) __attribute__((always_inline)) { issue(pb, args.ldB, PB, r, z); };
-  auto stage_head = [&](int l, int z) __attribute__((always_inline)) {
-    stage(pa, args.stA, PA, args.maskA[l], z);
+  auto issue_head = [&](int64_t r) __attribute__((always_inline)) { issue(pa, tab->ldA, PA, r); };
+  auto issue_tail = [&](int64_t r) __attribute__((always_inline)) { issue(pb, tab->ldB, PB, r); };
+  auto stage_head = [&](int l) __attribute__((always_inline)) {
+    stage(pa, tab->stA, PA, (uint32_t)__builtin_amdgcn_readfirstlane(tab->maskA[l]));
   };
-  auto stage_tail = [&](int z) __attribute__((always_inline)) { stage(pb, args.stB, PB, ~0u, z); };
+  auto stage_tail = [&]() __attribute__((always_inline)) {
+    stage(pb, tab->stB, PB, (1u << PB) - 1u);
+  };
   auto wait_loads = [&]() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
   // without prefetch: the bands of level l, NT * PB coefficients at a time through pb
   auto direct = [&](int l, int64_t r) __attribute__((always_inline)) {
-    const int src = args.lv[l].src, dbuf = args.lv[l].dbuf;
+    const int src = __builtin_amdgcn_readfirstlane(tab->lv[l].src);
+    const int dbuf = __builtin_amdgcn_readfirstlane(tab->lv[l].dbuf);
     for (int s = 0; s < 2; ++s) {
       if (s == 0 && l > 0) continue;  // a_0 belongs to level 0 only
       const S* band = static_cast<const S*>(args.band[s == 0 ? 0 : l + 1]);
@@ -1180,7 +1197,7 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
   // (always inlined: an outlined lambda would take the address of the kernel arguments, which
   // then get copied to private memory)
   auto level = [&](int l, int64_t row) __attribute__((always_inline)) {
-    const SynLevel lv = args.lv[l];
+    const SynLevel lv = lds_uniform(tab->lv + l);
     const bool last = l + 1 == J;
     // zero margins of both bands (and the whole band when it is absent)
     zero(lv.src, lv.src + ZL);
@@ -1261,23 +1278,21 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
   // would make the compiler copy the prefetch registers between paths, and every copy of a
   // register whose load is in flight waits for all loads)
   int64_t row = blockIdx.x;
-  if constexpr (PRE) issue_head(row, 0);
+  if constexpr (PRE) issue_head(row);
   for (; row < rows; row += gridDim.x) {
     const int64_t next = row + gridDim.x < rows ? row + gridDim.x : rows - 1;
-    int z = 0;
-    asm volatile("" : "+s"(z));
     if constexpr (PRE) {
       // levels 0 .. J-2: the head (requested before the previous row's last level) is
       // complete after this wait; this row's tail is requested here, waited for at level J-1
       wait_loads();
-      stage_head(0, z);
-      issue_tail(row, z);
+      stage_head(0);
+      issue_tail(row);
     } else {
       direct(0, row);
     }
     for (int l = 0; l + 1 < J; ++l) {
       if (l > 0) {
-        if constexpr (PRE) stage_head(l, z);
+        if constexpr (PRE) stage_head(l);
         else direct(l, row);
       }
       level(l, row);
@@ -1286,8 +1301,8 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
     // duration covers its latency
     if constexpr (PRE) {
       wait_loads();
-      stage_tail(z);
-      issue_head(next, z);
+      stage_tail();
+      issue_head(next);
     } else if (J > 1) {
       direct(J - 1, row);
     }
@@ -1601,7 +1616,7 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
   auto r4 = [](int64_t v) { return (v + 3) & ~(int64_t)3; };
   const int64_t yP = 0, yQ = r4(capP), yD = yQ + r4(capQ), yE = yD + r4(capD);
   const int64_t yT = yE + r4(capE);
-  const size_t lds = (size_t)(yT + r4(2 * L)) * cs;
+  const size_t lds = sizeof(SynTab) + (size_t)(yT + r4(2 * L)) * cs;
   if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
 
   SynArgs a{};
@@ -1610,7 +1625,7 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
     a.band[l + 1] = s.details[l];
     a.nc[l] = s.nc[l];
     const SynGeom& g = geo[l];
-    SynLevel& r = a.lv[l];
+    SynLevel& r = a.tab.lv[l];
     r.m = g.m;
     r.mw = g.mw;
     r.md = g.md;
@@ -1636,18 +1651,18 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
         const int es = dtype_size(dtype);
         const SynLoad ld{static_cast<const char*>(band) + (size_t)c0 * es, s.nc[l] * es, cnt};
         if (tail) {
-          a.ldB[k] = ld;
-          a.stB[k] = syn_stage_word(dest, cnt);
+          a.tab.ldB[k] = ld;
+          a.tab.stB[k] = syn_stage_word(dest, cnt);
         } else {
-          a.ldA[k] = ld;
-          a.stA[k] = syn_stage_word(dest, cnt);
-          a.maskA[l] |= 1u << k;
+          a.tab.ldA[k] = ld;
+          a.tab.stA[k] = syn_stage_word(dest, cnt);
+          a.tab.maskA[l] |= 1u << k;
         }
       });
   if (!pre) {  // no prefetch: clear whatever was filled before the overflow
-    for (int k = 0; k < PA; ++k) a.ldA[k] = SynLoad{nullptr, 0, 0}, a.stA[k] = 0;
-    for (int k = 0; k < PB; ++k) a.ldB[k] = SynLoad{nullptr, 0, 0}, a.stB[k] = 0;
-    for (int l = 0; l < J; ++l) a.maskA[l] = 0;
+    for (int k = 0; k < PA; ++k) a.tab.ldA[k] = SynLoad{nullptr, 0, 0}, a.tab.stA[k] = 0;
+    for (int k = 0; k < PB; ++k) a.tab.ldB[k] = SynLoad{nullptr, 0, 0}, a.tab.stB[k] = 0;
+    for (int l = 0; l < J; ++l) a.tab.maskA[l] = 0;
   }
   a.out = s.out;
   a.h0 = s.h0;
