@@ -283,8 +283,13 @@ def test_fp32_attention_matches_fp64():
         (y * torch.cos(torch.arange(y.numel(), device=DEV, dtype=dt).view_as(y))).sum().backward()
         outs.append([t.detach().double() for t in (y, xx.grad, mm.freq_weight.grad,
                                                     mm.cwt.log_scales.grad, mm.cwt.w0.grad)])
-    for a, b in zip(*outs):
-        torch.testing.assert_close(b, a, rtol=1e-4, atol=1e-5 * a.abs().max().item())
+    # y and x.grad: 1e-5 of the max.  The parameter gradients are sums over every position of
+    # every row; there the reference algorithm's own fp32 CPU path (oracle/, same problem,
+    # float32 vs float64) misses by up to 1.6e-5 of the max (freq_weight.grad), so they get
+    # 3e-5 of the max.
+    for k, (a, b) in enumerate(zip(*outs)):
+        frac = 1e-5 if k < 2 else 3e-5
+        torch.testing.assert_close(b, a, rtol=1e-4, atol=frac * a.abs().max().item())
 
 
 def test_token_mixers_run_and_backprop():
