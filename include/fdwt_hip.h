@@ -112,6 +112,27 @@ int64_t fdwt_chain_max_length(int32_t taps, int32_t dtype);
  */
 #define FDWT_CWT_MAX_SCALES 64
 
+/* Sampled Morlet filter bank, replacing `MorletPlan.filters(scales, w0, dtype)`
+ * (src/fdwt/cwt.py:181-203) on the device: H (n_scales * channels, 2 center + 1) in dtype,
+ * row i * channels + ch, column center + k, for scale scales[i] sampled at spacing dil[i]
+ * and truncated to |k| <= support[i]; channels 2 = re / im rows, 1 = real only; norm_l2 = 1
+ * for the 1/sqrt(s) normalisation, 0 for 1/s.  scales (n_scales) and w0 (1) are float64
+ * device arrays, dil / support host arrays (n_scales <= FDWT_MORLET_MAX_FILTERS).  Values are
+ * computed in float64 at |k| and mirrored, so rows are exactly even (re) / odd (im). */
+#define FDWT_MORLET_MAX_FILTERS 256
+int fdwt_morlet_filters(const double* scales, const double* w0, const int32_t* dil,
+                        const int32_t* support, int32_t n_scales, int32_t center,
+                        int32_t channels, int32_t norm_l2, void* H, int32_t dtype, void* stream);
+
+/* Gradient of fdwt_morlet_filters, replacing autograd through the torch construction of
+ * cwt.py:181-203: writes g_scales[i] = sum_k gH[i, k] dH[i, k]/ds_i and
+ * g_w0[0] = sum gH dH/dw0 (float64 device arrays; gH in dtype, the shape of H).  One
+ * workgroup, fixed summation order (deterministic). */
+int fdwt_morlet_filters_backward(const double* scales, const double* w0, const int32_t* dil,
+                                 const int32_t* support, int32_t n_scales, int32_t center,
+                                 int32_t channels, int32_t norm_l2, const void* gH,
+                                 int32_t dtype, double* g_scales, double* g_w0, void* stream);
+
 /* replaces the half-band launcher `halfband(x, taps, y, off, dil, transpose, accumulate)`
  * (src/fdwt/kernels/conv.py:411-430):
  *   y[r, n] (+)= taps[0] x[r, n + b] + sum_{t odd <= c} taps[t] (x[r, n + b - dil t] + x[r, n + b + dil t])

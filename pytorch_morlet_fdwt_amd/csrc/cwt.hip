@@ -157,18 +157,44 @@ __global__ void __launch_bounds__(NT) morlet_backward_x_kernel(Stage st, const T
   const int64_t q0 = p0 - st.x_off - (int64_t)dil * half;  // g position of G[0]
   const T* taps = static_cast<const T*>(st.taps);
   const int tid = threadIdx.x;
+  const int nel = span * C;
   T acc[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) acc[v] = T(0);
+  // The g tile of the next scale is loaded into registers while the current one is used (its
+  // first GPF * NT elements; a longer tile loads the rest when it is staged).
+  constexpr int GPF = sizeof(T) == 8 ? 4 : 8;
+  T gr[GPF];
+  auto fetch = [&](int s) {
+    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out) * C;
+#pragma unroll
+    for (int r = 0; r < GPF; ++r) {
+      const int k = tid + r * NT;
+      if (r * NT < nel) {
+        const int64_t q = q0 + k / C;
+        gr[r] = grow[min(max(q, (int64_t)0), st.n_out - 1) * C + (k % C)];
+      }
+    }
+  };
+  if (st.n_scales > 0) fetch(0);
   for (int s = 0; s < st.n_scales; ++s) {
     const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out) * C;
     __syncthreads();
-    for (int k = tid; k < span * C; k += NT) {
+#pragma unroll
+    for (int r = 0; r < GPF; ++r) {
+      const int k = tid + r * NT;
+      if (r * NT < nel && k < nel) {
+        const int64_t q = q0 + k / C;
+        G[k] = (q >= 0 && q < st.n_out) ? gr[r] : T(0);
+      }
+    }
+    for (int k = GPF * NT + tid; k < nel; k += NT) {
       const int64_t q = q0 + k / C;
       const T w = grow[min(max(q, (int64_t)0), st.n_out - 1) * C + (k % C)];
       G[k] = (q >= 0 && q < st.n_out) ? w : T(0);
     }
     __syncthreads();
+    if (s + 1 < st.n_scales) fetch(s + 1);
     const int tmax = st.sup[s];
     const T* tp = taps + s * (half + 1) * C;
     const int base = tid + dil * half;
@@ -689,6 +715,116 @@ __global__ void __launch_bounds__(NT) reduce_cols_kernel(const T* __restrict__ i
   }
 }
 
+// ------------------------------------------------------------------ filter synthesis
+// Sampled Morlet filters (reference cwt.py:181-203): row i C + ch, column center + k,
+//   t = k dil_i / s_i,  env = exp(-t^2 / 2) [|k| <= sup_i],  amp = pi^(-1/4) dil_i / s_i^p,
+//   re = (cos(w0 t) - exp(-w0^2 / 2)) env amp,   im = sin(w0 t) env amp,
+// with p = 1/2 (l2 norm) or 1 (l1).  Every value is computed at a = |k| in float64 and
+// written to both sides, so real rows are exactly even and imaginary rows exactly odd (the
+// bank kernels above rely on that).  The gradient kernel applies the derivatives
+//   s d re/ds  = env amp [w0 t sin(w0 t) + (cos(w0 t) - e)(t^2 - p)],     e = exp(-w0^2 / 2)
+//   s d im/ds  = env amp [sin(w0 t)(t^2 - p) - w0 t cos(w0 t)]
+//   d re/dw0   = env amp [w0 e - t sin(w0 t)],   d im/dw0 = env amp t cos(w0 t)
+// to the pair sums gH[c + a] + gH[c - a] (real rows) and differences gH[c + a] - gH[c - a]
+// (imaginary rows); one wave reduces one scale, so the result is deterministic.
+constexpr int MAXF = FDWT_MORLET_MAX_FILTERS;
+constexpr double PI_M14 = 0.75112554446494248286;  // pi^(-1/4)
+
+struct FilterArgs {
+  const double* scales;  // (n_scales) device
+  const double* w0;      // (1) device
+  int32_t n_scales, center, C, l2;
+  int32_t dil[MAXF];
+  int32_t sup[MAXF];
+};
+
+// The per-scale tables are indexed per lane, so they are read in place from the kernel
+// argument segment (a by-value copy indexed at run time would go to scratch).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define FDWT_FILTER_ARGS(name)                                              \
+  typedef __attribute__((address_space(4))) const FilterArgs FArgs_;         \
+  FArgs_& name = *(FArgs_*)__builtin_amdgcn_kernarg_segment_ptr()
+#else
+#define FDWT_FILTER_ARGS(name) const FilterArgs& name = *static_cast<const FilterArgs*>(nullptr)
+#endif
+
+struct MorletSample {
+  double t, env_amp, c, sn;  // t, env * amp, cos(w0 t), sin(w0 t)
+};
+
+__device__ inline MorletSample morlet_sample(double s, double w0, int dil, int sup, int l2,
+                                             int a) {
+  MorletSample m;
+  m.t = (double)a * (double)dil / s;
+  const double env = a <= sup ? exp(-0.5 * m.t * m.t) : 0.0;
+  m.env_amp = env * (PI_M14 * (double)dil / (l2 ? sqrt(s) : s));
+  sincos(w0 * m.t, &m.sn, &m.c);
+  return m;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(NT) morlet_filters_kernel(FilterArgs, T* __restrict__ H) {
+  FDWT_FILTER_ARGS(fa);
+  const int w = fa.center + 1;
+  const int64_t e = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (e >= (int64_t)fa.n_scales * w) return;
+  const int i = (int)(e / w), a = (int)(e % w);
+  const double w0 = fa.w0[0];
+  const MorletSample m = morlet_sample(fa.scales[i], w0, fa.dil[i], fa.sup[i], fa.l2, a);
+  const double re = (m.c - exp(-0.5 * w0 * w0)) * m.env_amp;
+  const int W = 2 * fa.center + 1;
+  T* row = H + (int64_t)i * fa.C * W + fa.center;
+  row[a] = T(re);
+  row[-a] = T(re);
+  if (fa.C == 2) {
+    const double im = m.sn * m.env_amp;
+    row[W + a] = T(im);
+    if (a > 0) row[W - a] = T(-im);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(NT) morlet_filters_backward_kernel(FilterArgs,
+                                                                     const T* __restrict__ gH,
+                                                                     double* __restrict__ g_scales,
+                                                                     double* __restrict__ g_w0) {
+  FDWT_FILTER_ARGS(fa);
+  __shared__ double w0_part[NT / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int W = 2 * fa.center + 1;
+  const double w0 = fa.w0[0];
+  const double ew = exp(-0.5 * w0 * w0);
+  const double p = fa.l2 ? 0.5 : 1.0;
+  double gw = 0.0;
+  for (int i = wave; i < fa.n_scales; i += NT / 64) {
+    const double s = fa.scales[i];
+    const T* row = gH + (int64_t)i * fa.C * W + fa.center;
+    double gs = 0.0;
+    for (int a = lane; a <= fa.center; a += 64) {
+      const MorletSample m = morlet_sample(s, w0, fa.dil[i], fa.sup[i], fa.l2, a);
+      const double gr = a ? (double)row[a] + (double)row[-a] : (double)row[0];
+      const double tt = m.t * m.t - p;
+      gs += gr * m.env_amp * (w0 * m.t * m.sn + (m.c - ew) * tt);
+      gw += gr * m.env_amp * (w0 * ew - m.t * m.sn);
+      if (fa.C == 2 && a > 0) {
+        const double gi = (double)row[W + a] - (double)row[W - a];
+        gs += gi * m.env_amp * (m.sn * tt - w0 * m.t * m.c);
+        gw += gi * m.env_amp * m.t * m.c;
+      }
+    }
+    for (int d = 32; d > 0; d >>= 1) gs += __shfl_xor(gs, d);
+    if (lane == 0) g_scales[i] = gs / s;
+  }
+  for (int d = 32; d > 0; d >>= 1) gw += __shfl_xor(gw, d);
+  if (lane == 0) w0_part[wave] = gw;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int v = 0; v < NT / 64; ++v) t += w0_part[v];
+    g_w0[0] = t;
+  }
+}
+
 // ------------------------------------------------------------------ host helpers
 int fill_stage(Stage& st, const void* x, const void* taps, int64_t n_in, int64_t n_out,
                int64_t x_off, int32_t n_scales, int32_t half, const int32_t* support,
@@ -1065,4 +1201,59 @@ extern "C" int fdwt_softmax_backward(const void* x, const void* taps, const void
   FDWT_LDS_ONCE(k);
   return launch(k, rows * tiles, lds, hs, st, sa, (const double*)m, (const double*)l,
                 (const double*)out, (const double*)gy, (double*)gw, (double*)workspace, tiles);
+}
+
+
+// ------------------------------------------------------------------ filter synthesis (host)
+static int fill_filter_args(FilterArgs& fa, const double* scales, const double* w0,
+                            const int32_t* dil, const int32_t* support, int32_t n_scales,
+                            int32_t center, int32_t channels, int32_t norm_l2, int32_t dtype) {
+  if (!scales || !w0 || !dil || !support || n_scales < 1 || n_scales > MAXF || center < 0 ||
+      (channels != 1 && channels != 2) || (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  fa.scales = scales;
+  fa.w0 = w0;
+  fa.n_scales = n_scales;
+  fa.center = center;
+  fa.C = channels;
+  fa.l2 = norm_l2 ? 1 : 0;
+  for (int i = 0; i < MAXF; ++i) {
+    fa.dil[i] = i < n_scales ? dil[i] : 1;
+    fa.sup[i] = i < n_scales ? support[i] : 0;
+    if (i < n_scales && (dil[i] < 1 || support[i] < 0)) return FDWT_ERR_ARG;
+  }
+  return 0;
+}
+
+extern "C" int fdwt_morlet_filters(const double* scales, const double* w0, const int32_t* dil,
+                                   const int32_t* support, int32_t n_scales, int32_t center,
+                                   int32_t channels, int32_t norm_l2, void* H, int32_t dtype,
+                                   void* stream) {
+  FilterArgs fa;
+  int e = fill_filter_args(fa, scales, w0, dil, support, n_scales, center, channels, norm_l2,
+                           dtype);
+  if (e) return e;
+  if (!H) return FDWT_ERR_ARG;
+  const int64_t blocks = cdiv((int64_t)n_scales * (center + 1), NT);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (dtype == FDWT_F32) return launch(morlet_filters_kernel<float>, blocks, 0, hs, fa, (float*)H);
+  return launch(morlet_filters_kernel<double>, blocks, 0, hs, fa, (double*)H);
+}
+
+extern "C" int fdwt_morlet_filters_backward(const double* scales, const double* w0,
+                                            const int32_t* dil, const int32_t* support,
+                                            int32_t n_scales, int32_t center, int32_t channels,
+                                            int32_t norm_l2, const void* gH, int32_t dtype,
+                                            double* g_scales, double* g_w0, void* stream) {
+  FilterArgs fa;
+  int e = fill_filter_args(fa, scales, w0, dil, support, n_scales, center, channels, norm_l2,
+                           dtype);
+  if (e) return e;
+  if (!gH || !g_scales || !g_w0) return FDWT_ERR_ARG;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (dtype == FDWT_F32)
+    return launch(morlet_filters_backward_kernel<float>, 1, 0, hs, fa, (const float*)gH,
+                  g_scales, g_w0);
+  return launch(morlet_filters_backward_kernel<double>, 1, 0, hs, fa, (const double*)gH,
+                g_scales, g_w0);
 }

@@ -130,6 +130,22 @@ class MorletPlan:
         st = self.stages[k]
         return [i * self.channels + c for i in st.scale_idx for c in range(self.channels)]
 
+    def filter_geometry(self):
+        """Per-scale dilation and half support as ctypes int32 arrays (filter kernels)."""
+        if "geom" not in self._cache:
+            self._cache["geom"] = (_i32([int(d) for d in self._dil]),
+                                   _i32([int(c) for c in self._sup]))
+        return self._cache["geom"]
+
+    def w0_device(self, w0, device: torch.device) -> torch.Tensor:
+        """w0 as a float64 device scalar (a tensor is converted on the device, no sync)."""
+        if isinstance(w0, torch.Tensor):
+            return w0.detach().to(device=device, dtype=torch.float64).reshape(1).contiguous()
+        key = ("w0", float(w0), device)
+        if key not in self._cache:
+            self._cache[key] = torch.tensor([float(w0)], dtype=torch.float64, device=device)
+        return self._cache[key]
+
     def halfband_taps(self, device: torch.device, dtype: torch.dtype) -> torch.Tensor:
         """``taps[t] = lowpass[c_lp + t]`` (t = 0..c_lp), as used by the half-band kernel."""
         key = ("hb", device, dtype)
@@ -154,7 +170,11 @@ class MorletPlan:
         """All sampled Morlet filters as one ``(S*C, 2*center+1)`` tensor (row ``i*C + c``),
         reference cwt.py:181-203.  Built on k >= 0 and mirrored, so the real rows are exactly
         even and the imaginary rows exactly odd (the HIP kernels rely on that symmetry).
-        Differentiable w.r.t. ``scales`` and ``w0`` (when it is a tensor)."""
+        Differentiable w.r.t. ``scales`` and ``w0`` (when it is a tensor).  On a ROCm device
+        one HIP kernel builds the bank and one computes its gradient; on the CPU (host-side
+        planning and inspection) it is the torch expression below."""
+        if scales.is_cuda:
+            return _MorletFiltersFunction.apply(scales, w0, self, dtype)
         dev = scales.device
         f64 = torch.float64
         s = scales.to(f64)[:, None]
@@ -173,6 +193,50 @@ class MorletPlan:
         im = torch.sin(w0t) * env * amp
         im = torch.cat([-im[:, 1:].flip(-1), im], 1)
         return torch.stack([re, im], 1).reshape(-1, re.shape[1]).to(dtype)
+
+
+class _MorletFiltersFunction(torch.autograd.Function):
+    """Device filter bank: ``fdwt_morlet_filters`` (forward) and
+    ``fdwt_morlet_filters_backward`` (gradient w.r.t. scales and w0), reference
+    cwt.py:181-203.  ``w0`` is a float or a tensor; its gradient is returned in the latter
+    case."""
+
+    @staticmethod
+    def forward(ctx, scales, w0, plan: "MorletPlan", dtype):
+        dev = scales.device
+        s = scales.detach().to(torch.float64).contiguous()
+        w = plan.w0_device(w0, dev)
+        H = torch.empty((plan.num_scales * plan.channels, 2 * plan.center + 1), device=dev,
+                        dtype=_out_dtype(dtype))
+        dil, sup = plan.filter_geometry()
+        _lib.launch("fdwt_morlet_filters", dev, _lib.ptr(s), _lib.ptr(w), dil, sup,
+                    plan.num_scales, plan.center, plan.channels, int(plan.norm == "l2"),
+                    _lib.ptr(H), _lib.dtype_code(H.dtype), _lib.stream(dev))
+        ctx.plan, ctx.w0_tensor = plan, isinstance(w0, torch.Tensor)
+        ctx.scales_dtype = scales.dtype
+        ctx.w0_meta = (w0.dtype, w0.shape) if ctx.w0_tensor else None
+        ctx.save_for_backward(s, w)
+        return H if H.dtype == dtype else H.to(dtype)
+
+    @staticmethod
+    def backward(ctx, gH):
+        plan: MorletPlan = ctx.plan
+        s, w = ctx.saved_tensors
+        dev = s.device
+        gH = gH.contiguous()
+        if gH.dtype not in (torch.float32, torch.float64):
+            gH = gH.float()
+        g = torch.empty(plan.num_scales + 1, device=dev, dtype=torch.float64)
+        dil, sup = plan.filter_geometry()
+        _lib.launch("fdwt_morlet_filters_backward", dev, _lib.ptr(s), _lib.ptr(w), dil, sup,
+                    plan.num_scales, plan.center, plan.channels, int(plan.norm == "l2"),
+                    _lib.ptr(gH), _lib.dtype_code(gH.dtype), _lib.ptr(g),
+                    _lib.ptr(g[plan.num_scales:]), _lib.stream(dev))
+        g_s = g[:plan.num_scales].to(ctx.scales_dtype)
+        g_w0 = None
+        if ctx.w0_tensor:
+            g_w0 = g[plan.num_scales].to(ctx.w0_meta[0]).reshape(ctx.w0_meta[1])
+        return g_s, g_w0, None, None
 
 
 # --------------------------------------------------------------------------- stage launches

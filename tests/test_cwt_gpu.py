@@ -314,3 +314,61 @@ def test_token_mixers_run_and_backprop():
 def test_channel_mix_attention_map():
     m = fdwt.MorletChannelMixAttention(num_channels=5, hidden_dim=64).to(DEV)
     assert m.attention_map(torch.randn(2, 3, 5, 6, 64, device=DEV)).shape == (2, 3, 6 * 64, 5, 5)
+
+
+FILTER_PLANS = {
+    "complex_l2": dict(scales=[1.5, 3.0, 7.0, 30.0, 90.0], support_margin=1.25),
+    "real_l1": dict(scales=[2.0, 5.0, 11.0, 40.0], norm="l1", complex=False),
+    "w5_t5": dict(scales=list(np.geomspace(1.2, 200.0, 19)), w0=5.0, truncate=5.0),
+}
+
+
+@pytest.mark.parametrize("name", sorted(FILTER_PLANS))
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_device_filters_match_oracle(name, dtype):
+    """The filter-bank kernel against the oracle's direct construction of cwt.py:181-203
+    (values), and its gradient kernel against autograd through that construction."""
+    kw = dict(FILTER_PLANS[name])
+    scales = kw.pop("scales")
+    p = fdwt.MorletPlan(scales, **kw)
+    op = O.Plan(scales, w0=kw.get("w0", 6.0), truncate=kw.get("truncate", 4.0),
+                norm=kw.get("norm", "l2"), complex=kw.get("complex", True),
+                support_margin=kw.get("support_margin", 1.0))
+    gen = torch.Generator().manual_seed(7)
+    ls = (torch.tensor(scales, dtype=f64).log() + 0.05 * torch.randn(len(scales), generator=gen))
+    w0v = p.w0 + 0.3
+    ls_c = ls.clone().requires_grad_()
+    w0_c = torch.tensor(w0v, dtype=f64, requires_grad=True)
+    ref = op.filters(ls_c.exp(), w0_c)
+    ls_g = ls.to(DEV).requires_grad_()
+    w0_g = torch.tensor(w0v, dtype=f64, device=DEV, requires_grad=True)
+    H = p.filters(ls_g.exp(), w0_g, dtype)
+    assert H.shape == ref.shape and H.dtype == dtype
+    tol = 1e-14 if dtype == f64 else 1e-7
+    scale = float(ref.abs().max())
+    torch.testing.assert_close(H.detach().cpu().double(), ref.detach(), rtol=0, atol=tol * scale)
+    # exact symmetry of the device bank
+    C = p.channels
+    Hc = H.detach().cpu()
+    assert torch.equal(Hc[0::C], Hc[0::C].flip(-1))
+    if C == 2:
+        assert torch.equal(Hc[1::2], -Hc[1::2].flip(-1))
+    gH = torch.randn(ref.shape, dtype=f64, generator=gen)
+    g_ls, g_w0 = torch.autograd.grad(ref, (ls_c, w0_c), gH)
+    d_ls, d_w0 = torch.autograd.grad(H, (ls_g, w0_g), gH.to(DEV, dtype))
+    gtol = 1e-12 if dtype == f64 else 1e-5
+    gscale = float(max(g_ls.abs().max(), g_w0.abs()))
+    torch.testing.assert_close(d_ls.cpu(), g_ls, rtol=0, atol=gtol * gscale)
+    torch.testing.assert_close(d_w0.cpu(), g_w0, rtol=0, atol=gtol * gscale)
+
+
+def test_device_filters_gradcheck():
+    """Finite differences pin the analytic derivatives of the gradient kernel."""
+    p = fdwt.MorletPlan([1.7, 4.0, 9.0, 25.0], support_margin=1.25)
+    ls = torch.tensor(p.scales, dtype=f64, device=DEV).log().requires_grad_()
+    w0 = torch.tensor(6.2, dtype=f64, device=DEV, requires_grad=True)
+    assert gradcheck(lambda a, b: p.filters(a.exp(), b, f64), (ls, w0), eps=1e-6, atol=1e-8)
+    # a float w0 gets no gradient and the scales still do
+    H = p.filters(ls.exp(), 6.0, f64)
+    (g,) = torch.autograd.grad(H.square().sum(), ls)
+    assert torch.isfinite(g).all() and g.abs().max() > 0
