@@ -238,6 +238,13 @@ inline bool syn_regs(int J, const int32_t* nc, const void* approx, const void* c
 // Load element i of a global array whose pointer the compiler cannot place in the global
 // address space (e.g. one read from LDS): a generic (flat) load would also count against the
 // LDS wait counter, so every later LDS wait would wait for it too.
+// One 16-byte-aligned group of four floats through a global (not flat) pointer.
+typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+__device__ inline v4u_t global_load16(const float* p) {
+  typedef __attribute__((address_space(1))) const v4u_t* gptr;
+  return *(gptr)p;
+}
+
 template <typename S>
 __device__ inline S global_load(const S* p, int64_t i) {
   typedef typename std::conditional<
@@ -609,7 +616,119 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
       }
     };
 
-    if (LT > 0 || L <= MAXL_T) {
+    if constexpr (std::is_same<S, float>::value && std::is_same<T, float>::value && LT > 0) {
+      // fp32 rows: the window B[idx] = x[p0 + idx] is loaded as 16-byte-aligned groups of four
+      // samples, group g holding positions q0 + 4 g + j (q0 = p0 - d aligned down); B has a
+      // guard of four elements on either side for the parts of the end groups outside the
+      // window.  Only groups lying inside the row [gf, gl] are staged from these loads (every
+      // lane loads one, clamped into that range, so each register is written in full and the
+      // compiler never waits for it); the window positions outside them -- the extension
+      // near the row ends, at most 3 + (L - 1 - off) on the left and 2 L + 6 on the right --
+      // are loaded one per thread by the first FX threads at their extension index.
+      constexpr int SPAN = 2 * CO + LT - 2;
+      constexpr int PW = ((SPAN + 6) / 4 + NT - 1) / NT;
+      constexpr int FX = 128;
+      typedef float v4f __attribute__((ext_vector_type(4)));
+      typedef float v2f __attribute__((ext_vector_type(2)));
+      v4u_t w[PW];
+      unsigned fx = 0u;
+      const unsigned xa = (unsigned)(reinterpret_cast<uintptr_t>(xrow) >> 2);
+      const int pmax = 2 * (no - 1) + off;  // last position any output of the level reads
+      struct Geo {
+        int p0, q0, d, G, gf, gl, nl, r0, nfix;
+      };
+      auto geom = [&](int c) {
+        Geo g;
+        g.p0 = 2 * c * CO + pmin;
+        g.d = (int)((xa + (unsigned)g.p0) & 3u);
+        g.q0 = g.p0 - g.d;
+        g.G = (SPAN + g.d + 3) >> 2;
+        g.gf = g.q0 >= 0 ? 0 : (3 - g.q0) >> 2;
+        g.gl = min(g.G - 1, (n - 4 - g.q0) >> 2);
+        const int pend = min(g.p0 + SPAN, pmax + 1);  // window positions read: [p0, pend)
+        if (g.gf <= g.gl) {
+          g.nl = max(0, min(g.q0 + 4 * g.gf, pend) - g.p0);
+          g.r0 = max(g.p0, g.q0 + 4 * (g.gl + 1));
+          g.nfix = g.nl + max(0, pend - g.r0);
+        } else {
+          g.nl = max(0, pend - g.p0);
+          g.r0 = pend;
+          g.nfix = g.nl;
+        }
+        g.nfix = min(g.nfix, FX);
+        return g;
+      };
+      auto fetch4 = [&](int c) {
+        const Geo g = geom(c);
+        if (g.gf <= g.gl) {
+#pragma unroll
+          for (int k = 0; k < PW; ++k)
+            if (k * NT < g.G)
+              w[k] = global_load16(xrow + g.q0 + 4 * min(max(tid + k * NT, g.gf), g.gl));
+        }
+        if (tid < FX && g.nfix > 0) {
+          const int t = min(tid, g.nfix - 1);
+          const int p = t < g.nl ? g.p0 + t : g.r0 + (t - g.nl);
+          int i = min(max(p, 0), n - 1);
+          if (p < 0 || p >= n) {
+            bool valid = true;
+            i = ext_index(p, n, mode0, P, valid);
+            if (!valid) i = 0;
+          }
+          fx = global_load(reinterpret_cast<const unsigned*>(xrow), i);
+        }
+      };
+      auto stage4 = [&](int c) {
+        const Geo g = geom(c);
+        // every prefetch register counts as used here, on every path, so that the compiler's
+        // wait for the loads sits here and not before the next chunk's loads
+#pragma unroll
+        for (int k = 0; k < PW; ++k) __asm__ volatile("" : : "v"(w[k]));
+        __asm__ volatile("" : : "v"(fx));
+        if (g.gf <= g.gl) {
+#pragma unroll
+          for (int k = 0; k < PW; ++k) {
+            const int gi = tid + k * NT;
+            if (k * NT < g.G && gi >= g.gf && gi <= g.gl) {
+              const v4f v = __builtin_bit_cast(v4f, w[k]);
+              float* dst = B + 4 * gi - g.d;
+              if (g.d == 0) {
+                *reinterpret_cast<v4f*>(dst) = v;
+              } else if (g.d == 2) {
+                *reinterpret_cast<v2f*>(dst) = v2f{v[0], v[1]};
+                *reinterpret_cast<v2f*>(dst + 2) = v2f{v[2], v[3]};
+              } else {  // d = 1 or 3: dst + 1 is 8-byte aligned
+                dst[0] = v[0];
+                *reinterpret_cast<v2f*>(dst + 1) = v2f{v[1], v[2]};
+                dst[3] = v[3];
+              }
+            }
+          }
+        }
+        if (tid < g.nfix) {
+          const int p = tid < g.nl ? g.p0 + tid : g.r0 + (tid - g.nl);
+          const float v = __builtin_bit_cast(float, fx);
+          B[p - g.p0] = (mode0 == FDWT_MODE_ZERO && (p < 0 || p >= n)) ? 0.0f : v;
+        }
+      };
+      if (c_begin < c_end) fetch4(c_begin);
+      for (int c = c_begin; c < c_end; ++c) {
+        __syncthreads();
+        stage4(c);
+        __syncthreads();
+        if (c + 1 < c_end) fetch4(c + 1);
+#pragma unroll
+        for (int g = 0; g < GA; ++g) {
+          const int lo = (g * NT + tid) * VA;  // output offset inside the chunk
+          const int o = c * CO + lo;
+          if (o >= no) break;
+          T y0[VA], y1[VA];
+          analysis_pair<T, LT>(B + 2 * lo, hr0, hr1, L, y0, y1);
+          store_bands<S, T>(drow, arow, last ? nullptr : A - pmin, o, no, y0, y1, vec_g,
+                            vec_l);
+        }
+      }
+    } else if (LT > 0 || L <= MAXL_T) {
       if (c_begin < c_end) fetch(c_begin, pf);
       for (int c = c_begin; c < c_end; ++c) {
         __syncthreads();
@@ -1479,13 +1598,16 @@ inline bool valid_common(int64_t rows, int taps, int mode, int dtype) {
 // level 0 and the inputs of even levels >= 2; sizes in compute elements.
 void achain_caps(const int64_t* n_in, const int64_t* n_out, int levels, int L, int* capA,
                  int* capB) {
-  const int64_t stage = 2 * (int64_t)CO + (L > MAXL_T ? L : MAXL_T) - 2;
+  // the level-0 window is staged in aligned groups of four: up to three elements before B
+  // (the last four elements of A are a guard) and three after the window
+  const int64_t stage = 2 * (int64_t)CO + (L > MAXL_T ? L : MAXL_T) - 2 + 4;
   int64_t a = 0, b = stage;
   for (int l = 1; l < levels; ++l) {
     const int64_t need = std::max<int64_t>(2 * n_out[l] + L, n_in[l] + L) + 2;
     if (l % 2) a = std::max(a, need);
     else b = std::max(b, need);
   }
+  a += 4;
   *capA = (int)((a + 3) & ~3);
   *capB = (int)((b + 3) & ~3);
 }
