@@ -36,6 +36,7 @@ __all__ = ["cwt", "CWT1D", "MorletPlan", "freqs_to_scales", "scales_to_freqs", "
            "spectral_softmax"]
 
 _PI_M14 = math.pi ** -0.25
+_MAX_FILTERS = 256  # FDWT_MORLET_MAX_FILTERS
 _MAX_STAGE_SCALES = 64  # FDWT_CWT_MAX_SCALES
 
 
@@ -174,6 +175,9 @@ class MorletPlan:
         one HIP kernel builds the bank and one computes its gradient; on the CPU (host-side
         planning and inspection) it is the torch expression below."""
         if scales.is_cuda:
+            if self.num_scales > _MAX_FILTERS:
+                raise ValueError(f"at most {_MAX_FILTERS} scales per Morlet bank on the device, "
+                                 f"got {self.num_scales}")
             return _MorletFiltersFunction.apply(scales, w0, self, dtype)
         dev = scales.device
         f64 = torch.float64
