@@ -581,8 +581,10 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
     const bool last = args.levels == 1;
     S* arow = last ? static_cast<S*>(args.approx) + row * (int64_t)no : nullptr;
 
-    // paired (8-byte) stores when rows stay 8-byte aligned: o is always even
-    const bool vec_g = std::is_same<S, float>::value && (no % 2) == 0;
+    // paired stores where this row's band starts 8-byte aligned (o is always even)
+    const bool vec_g =
+        std::is_same<S, float>::value &&
+        ((reinterpret_cast<uintptr_t>(drow) | reinterpret_cast<uintptr_t>(arow)) & 7) == 0;
     const bool vec_l = (pmin & 1) == 0;
     const int nchunks = (int)cdiv(no, CO);
     int c_begin = 0, c_end = nchunks;
@@ -800,7 +802,10 @@ __global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int
     const bool last = l + 1 == args.levels;
     S* drow = static_cast<S*>(args.details[l]) + row * (int64_t)no;
     S* arow = last ? static_cast<S*>(args.approx) + row * (int64_t)no : nullptr;
-    const bool vec_g = std::is_same<S, float>::value && (no % 2) == 0;
+    // paired stores where this row's band starts 8-byte aligned (o is always even)
+    const bool vec_g =
+        std::is_same<S, float>::value &&
+        ((reinterpret_cast<uintptr_t>(drow) | reinterpret_cast<uintptr_t>(arow)) & 7) == 0;
     const bool vec_l = (pmin & 1) == 0;
     for (int lo = tid * VA; lo < no; lo += NT * VA) {
       T y0[VA], y1[VA];
@@ -1332,8 +1337,13 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
     T* const E = lds + args.offE;
     T* const dst = last ? nullptr : lds + lv.dst + ZL;
     S* const orow = last ? static_cast<S*>(args.out) + row * (int64_t)m : nullptr;
-    const bool vec_out = std::is_same<S, float>::value && vec_lds && (m % 4) == 0;
-    const bool vec_shift = std::is_same<S, float>::value && sh != 0 && (m % 4) == 0;
+    // output rows: the shift to the next 16-byte boundary follows from the row's own address
+    // (rows of any length), LDS bands from the offset alone
+    const int osh = last ? (int)((4u - (((unsigned)(reinterpret_cast<uintptr_t>(orow) >> 2) +
+                                          (unsigned)(off - 1)) & 3u)) & 3u)
+                         : sh;
+    const bool vec_out = std::is_same<S, float>::value && osh == 0;
+    const bool vec_shift = std::is_same<S, float>::value && osh != 0;
     const int plo = lv.plo, phi = lv.phi, pbeg = lv.pbeg, pend = lv.pend;
     for (int vw = lv.vbeg + (tid - lane) * VR; vw < lv.vend; vw += NT * VR) {
       const int v0 = vw + lane * VR;
@@ -1351,7 +1361,7 @@ __global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
         // whole waves inside the plain range of the output row: shifted 16-byte stores
         const int iw = 2 * vw + off - 1;
         if (last && vec_shift && iw >= plo && iw + 128 * VR <= phi) {
-          store_shifted(orow, i0, v, sh, lane);
+          store_shifted(orow, i0, v, osh, lane);
           continue;
         }
       }
