@@ -144,14 +144,7 @@ def attention_flops(m, R, N):
     """Algorithmic FLOPs of one MorletAttention forward + backward (2 per real filter-tap
     MAC, unfolded taps, half-band chain included): forward = chain + filter bank; backward =
     chain recompute + bank recompute + grad-x + grad-h + transposed chain."""
-    plan = m.cwt.plan
-    bank = 0
-    for st in plan.stages:
-        for sup in st.support:
-            bank += 2 * 2 * (2 * sup + 1) * plan.channels * R * N
-    chain = 0
-    for j in range(plan.n_octaves - 1):
-        chain += 2 * (2 * plan.c_lp + 1) * R * (N + 2 * plan.margins[j + 1])
+    bank, chain = bank_chain_flops(m.cwt.plan, R, N)
     return 4 * bank + 3 * chain
 
 
@@ -225,6 +218,228 @@ def attention_cpu(batch=1, reps=3):
                       f"and w0, median of {reps} after 1 warm-up ({t:.2f} s per step)"}
 
 
+def _timed(step, steps, warmup):
+    """Mean ms per call of ``step`` over ``steps`` calls after ``warmup`` untimed ones
+    (torch events on the current stream, which is the stream every entry point launches on)."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _cpu_median(run, reps=3):
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    run()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), threads
+
+
+def bank_chain_flops(plan, R, N):
+    """(bank, chain) FLOPs of one pass of a plan over R rows of N samples: 2 per real
+    filter-tap MAC, unfolded taps, real and imaginary parts; the half-band chain over the
+    margins it runs on."""
+    bank = 0
+    for st in plan.stages:
+        for sup in st.support:
+            bank += 2 * plan.channels * (2 * sup + 1) * R * N
+    chain = 0
+    for j in range(plan.n_octaves - 1):
+        chain += 2 * (2 * plan.c_lp + 1) * R * (N + 2 * plan.margins[j + 1])
+    return bank, chain
+
+
+DWT1_SHAPE, DWT1_N, DWT1_LEVEL = (32, 64), 2500, 5  # BASELINE configs[0]
+
+
+def dwt_cfg1(steps, warmup, dev, cpu):
+    """wavedec(x, 'db4', 'symmetric', 5) -> waverec, forward plus
+    backward, x fp32 (32, 64, 2500)."""
+    import pytorch_morlet_fdwt_amd as fdwt
+    x = torch.randn(*DWT1_SHAPE, DWT1_N, generator=torch.Generator().manual_seed(0))
+    xd = x.to(dev).requires_grad_()
+    y0 = fdwt.waverec(fdwt.wavedec(xd, "db4", "symmetric", DWT1_LEVEL), "db4", "symmetric")
+    gy = torch.randn(y0.shape, generator=torch.Generator().manual_seed(1)).to(dev)
+
+    def step():
+        y = fdwt.waverec(fdwt.wavedec(xd, "db4", "symmetric", DWT1_LEVEL), "db4", "symmetric")
+        torch.autograd.grad(y, xd, gy)
+
+    ms = _timed(step, steps, warmup)
+    R = DWT1_SHAPE[0] * DWT1_SHAPE[1]
+    lens = coeff_lengths(DWT1_N, 8, "symmetric", DWT1_LEVEL)
+    C = sum(lens) + lens[-1]
+    m = y0.shape[-1]
+    byts = 4 * R * (2 * DWT1_N + 2 * m + 4 * C)
+    out = {"metric": "wavedec+waverec fwd+bwd GB/s (algorithmic HBM bytes / step time)",
+           "value": byts / (ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms,
+           "samples_per_s": R * DWT1_N / (ms * 1e-3),
+           "config": {"workload": "BASELINE configs[0]: db4, symmetric, level 5, x fp32 "
+                                  "(32,64,2500), waverec(wavedec(x)) fwd+bwd"},
+           "roofline": {"bound": "hbm", "achieved": byts / (ms * 1e-3) / 1e9,
+                        "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                        "frac": byts / (ms * 1e-3) / HBM_PEAK, "alg_bytes": byts}}
+    if cpu:
+        from oracle import dwt as O
+        rows = R  # the whole workload
+        xs = x.reshape(R, DWT1_N)[:rows].contiguous()
+        gys = gy.cpu().reshape(R, -1)[:rows].contiguous()
+
+        def run():
+            xx = xs.clone().requires_grad_()
+            y = O.waverec(O.wavedec(xx, "db4", "symmetric", DWT1_LEVEL), "db4", "symmetric")
+            torch.autograd.grad(y, xx, gys)
+
+        t, threads = _cpu_median(run)
+        out["cpu_baseline"] = {
+            "value": 4 * rows * (2 * DWT1_N + 2 * m + 4 * C) / t / 1e9, "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{rows} of {R} rows, fp32, median of 3 after 1 warm-up ({t:.3f} s)"}
+    return out
+
+
+CWT3_SHAPE, CWT3_N, CWT3_FS = (32, 64), 2500, 250.0  # BASELINE configs[2]
+
+
+def cwt3_signal(shape, n, gen):
+    t = torch.arange(n, dtype=torch.float32)
+    tone = sum(torch.sin(2 * torch.pi * f * t / CWT3_FS) for f in (6.0, 10.0, 18.0, 30.0))
+    return torch.randn(*shape, n, generator=gen) + tone
+
+
+def cwt_cfg3(steps, warmup, dev, cpu):
+    """fast Morlet CWT, 40 centre frequencies logspace(-0.3, 2) Hz at
+    fs = 250, w0 = 6, truncate = 4, l2 norm, learnable frequencies and w0; forward (complex64
+    scalogram (32, 64, 40, 2500)) plus backward on a random-normal upstream gradient."""
+    import pytorch_morlet_fdwt_amd as fdwt
+    freqs = torch.logspace(-0.3, 2, 40).tolist()
+    torch.manual_seed(2)
+    m = fdwt.CWT1D(freqs=freqs, fs=CWT3_FS, w0=6.0, truncate=4.0, norm="l2", learnable=True,
+                   learnable_w0=True).to(dev)
+    x = cwt3_signal(CWT3_SHAPE, CWT3_N, torch.Generator().manual_seed(0))
+    xd = x.to(dev).requires_grad_()
+    S = m.plan.num_scales
+    gen = torch.Generator(device=dev).manual_seed(1)
+    gy = torch.view_as_complex(torch.randn(*CWT3_SHAPE, S, CWT3_N, 2, generator=gen, device=dev))
+    params = [xd] + list(m.parameters())
+
+    def step():
+        y = m(xd)
+        torch.autograd.grad(y, params, gy)
+
+    ms = _timed(step, steps, warmup)
+    R = CWT3_SHAPE[0] * CWT3_SHAPE[1]
+    bank, chain = bank_chain_flops(m.plan, R, CWT3_N)
+    fl = 3 * bank + 2 * chain  # forward, grad-x and grad-h of the bank; chain and its transpose
+    byts = 4 * R * CWT3_N * 3 + 8 * R * S * CWT3_N * 2  # x twice, gx; W written, gW read
+    s = ms * 1e-3
+    out = {"metric": "Morlet CWT fwd+bwd samples/s (R*N per step)",
+           "value": R * CWT3_N / s, "unit": "samples/s", "ms_per_step": ms,
+           "gbps_alg": byts / s / 1e9, "frac_hbm_peak": byts / s / HBM_PEAK,
+           "config": {"workload": "BASELINE configs[2]: fast Morlet CWT, 40 freqs "
+                                  "logspace(-0.3,2) Hz, fs 250, w0 6, truncate 4, l2, learnable "
+                                  "freqs and w0, x fp32 (32,64,2500) N(0,1) + 6/10/18/30 Hz",
+                      "octaves": m.plan.n_octaves},
+           "roofline": {"bound": "valu", "achieved": fl / s / 1e12, "peak": FP32_PEAK / 1e12,
+                        "unit": "TFLOP/s", "frac": fl / s / FP32_PEAK, "alg_flops": fl,
+                        "alg_bytes": byts}}
+    if cpu:
+        from oracle import cwt as O
+        rows = 64
+        plan = O.Plan(m.plan.scales, w0=6.0, truncate=4.0, norm="l2", support_margin=1.25)
+        xs = x.reshape(R, CWT3_N)[:rows].contiguous()
+        ls = m.log_scales.detach().cpu().clone().requires_grad_()
+        w0 = torch.tensor(6.0, requires_grad=True)
+        g = torch.view_as_complex(torch.randn(rows, S, CWT3_N, 2,
+                                              generator=torch.Generator().manual_seed(1)))
+
+        def run():
+            xx = xs.clone().requires_grad_()
+            y = O.apply_plan(xx, plan, plan.filters(ls.double().exp(), w0.double(),
+                                                    torch.float32))
+            torch.autograd.grad(y, [xx, ls, w0], g)
+
+        t, threads = _cpu_median(run)
+        out["cpu_baseline"] = {"value": rows * CWT3_N / t, "unit": "samples/s",
+                               "cores": threads, "kind": "port",
+                               "sample": f"{rows} of {R} rows, fp32, median of 3 after 1 "
+                                         f"warm-up ({t:.3f} s)"}
+    return out
+
+
+MIX4_SHAPE, MIX4_DIM = (8, 4096, 256), 256  # BASELINE configs[3]
+
+
+def token_mixer_cfg4(steps, warmup, dev, cpu):
+    """MorletTokenMixer(dim=256, 16 freqs logspace(0, 1.8) Hz, fs=250),
+    Xavier-initialised mixing weights, input (8, 4096, 256) fp32; forward plus backward."""
+    import pytorch_morlet_fdwt_amd as fdwt
+    freqs = torch.logspace(0, 1.8, 16).tolist()
+    torch.manual_seed(2)
+    m = fdwt.MorletTokenMixer(MIX4_DIM, freqs=freqs, fs=250.0)
+    torch.nn.init.xavier_uniform_(m.mag_weight)
+    torch.nn.init.xavier_uniform_(m.phase_weight)
+    m = m.to(dev)
+    x = torch.randn(*MIX4_SHAPE, generator=torch.Generator().manual_seed(0))
+    xd = x.to(dev).requires_grad_()
+    gy = torch.randn(*MIX4_SHAPE, generator=torch.Generator().manual_seed(1)).to(dev)
+    params = [xd] + list(m.parameters())
+
+    def step():
+        y = m(xd)
+        torch.autograd.grad(y, params, gy)
+
+    ms = _timed(step, steps, warmup)
+    B, N, D = MIX4_SHAPE
+    R = B * D
+    bank, chain = bank_chain_flops(m.cwt.plan, R, N)
+    fl = 4 * bank + 3 * chain  # forward; backward recomputes W, then grad-x and grad-h
+    s = ms * 1e-3
+    out = {"metric": "MorletTokenMixer fwd+bwd tokens/s (B*L per step)",
+           "value": B * N / s, "unit": "tokens/s", "ms_per_step": ms,
+           "config": {"workload": "BASELINE configs[3]: MorletTokenMixer dim 256, 16 freqs "
+                                  "logspace(0,1.8) Hz, fs 250, Xavier mixing weights, x fp32 "
+                                  "(8,4096,256), out_proj included"},
+           "roofline": {"bound": "valu", "achieved": fl / s / 1e12, "peak": FP32_PEAK / 1e12,
+                        "unit": "TFLOP/s", "frac": fl / s / FP32_PEAK, "alg_flops": fl}}
+    if cpu:
+        from oracle import cwt as O
+        p = m.cwt.plan
+        plan = O.Plan(p.scales, support_margin=1.25)
+        rows = 64
+        xs = x[:1, :, :rows].contiguous()  # batch 1, `rows` of the 256 feature rows
+        ls = m.cwt.log_scales.detach().cpu().clone().requires_grad_()
+        a = m.mag_weight.detach().cpu()[:rows].clone().requires_grad_()
+        b = m.phase_weight.detach().cpu()[:rows].clone().requires_grad_()
+        bias = m.bias.detach().cpu()[:rows].clone().requires_grad_()
+        g = gy.cpu()[:1, :, :rows]
+
+        def run():
+            xx = xs.clone().requires_grad_()
+            y = O.token_mixer(xx, plan, plan.filters(ls.double().exp(), 6.0, torch.float32),
+                              a, b, bias)
+            torch.autograd.grad(y, [xx, ls, a, b, bias], g)
+
+        t, threads = _cpu_median(run)
+        out["cpu_baseline"] = {"value": N * rows / D / t, "unit": "tokens/s",
+                               "cores": threads, "kind": "port",
+                               "sample": f"batch 1 of {B}, {rows} of {D} feature rows (tokens "
+                                         f"counted pro rata), no out_proj, fp32, median of 3 "
+                                         f"after 1 warm-up ({t:.3f} s)"}
+    return out
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of ``kernel`` on this workload, as measured by the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated against a plain copy), or None."""
@@ -243,6 +458,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the configs[0], configs[2] and configs[3] legs")
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy (HBM counter calibration)")
@@ -324,6 +541,12 @@ def main():
         if not a.no_cpu_baseline:
             att["cpu_baseline"] = attention_cpu()
         line["morlet_attention"] = att
+    if not a.no_legs:
+        cpu = not a.no_cpu_baseline
+        k = max(3, a.steps // 2)
+        line["dwt_cfg1"] = dwt_cfg1(k, a.warmup, dev, cpu)
+        line["cwt_cfg3"] = cwt_cfg3(k, a.warmup, dev, cpu)
+        line["token_mixer_cfg4"] = token_mixer_cfg4(k, a.warmup, dev, cpu)
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(a.cpu_rows)
     print(json.dumps(line))
