@@ -220,6 +220,155 @@ __global__ void __launch_bounds__(NT) morlet_backward_x_kernel(Stage st, const T
   }
 }
 
+// ------------------------------------------------------------------ bank adjoint, windowed
+// The same adjoint for a power-of-two dilation, computed only where g reaches: gx[p] has a
+// contribution iff p - x_off lies in [-dil half, n_out - 1 + dil half], so the tiles cover
+// [lo, hi) = that range clipped to [0, n_in); positions outside it are left alone
+// (accumulate) or zeroed.
+//
+// Positions are p = lo + R + dil j (residue R < dil, j >= 0).  A tile takes D of the dil
+// residue classes (R0 .. R0 + D - 1) and J = TT / D consecutive j of each, and stages their
+// g values interleaved: tile element i = R_local + D jj holds g at q = lo - x_off + R0 +
+// R_local + dil (j0 + jj - H), jj < J + 2 H (H = half rounded up to RUN).  Neighbours in a
+// residue class are D apart in the tile, so the tap loop is the same for every dilation and
+// a small D keeps the halo (2 H D elements per tile) small next to the TT outputs.
+//
+// Thread (r, b) = (tid % D, tid / D) owns the RUN outputs j = j0 + RUN b + k, k < RUN, of
+// residue R0 + r.  With U_m = G[q_0 + D m] (q_0 = D H + r + D RUN b) output k needs U_{k+t}
+// and U_{k-t} at tap t, so two RUN-slot register windows (up: U_t .. U_{t+RUN-1}, down:
+// U_{-t} .. U_{RUN-1-t}) serve every output of the thread, and each tap loads just two new
+// values (one per window) into the slot the tap frees; the tap loop is unrolled by RUN so
+// every slot index is a compile-time constant.
+//
+// LDS layout: tile element i lives at phys(i) = i + D floor(i / (D RUN)), one step of
+// padding per thread run.  Because H is a multiple of RUN the runs align to that grid, so
+// phys(q_0 + D m) = phys(q_0) + D (m + floor(m / RUN)): loads are a per-thread base plus
+// immediate offsets, and the 32 lanes of a half-wave read 8-byte words in distinct banks for
+// every D (lane stride RUN + 1 words for D = 1).
+constexpr int RUN = V;  // outputs per thread; TT = NT RUN
+
+template <int D>
+__device__ inline int adj_phys(int i) {
+  constexpr int SH = __builtin_ctz(D * RUN);
+  return i + D * (i >> SH);
+}
+
+template <typename T, bool CPLX, int D>
+__global__ void __launch_bounds__(NT) morlet_adjoint_kernel(Stage st, const T* __restrict__ g,
+                                                            T* __restrict__ gx, int g_scales,
+                                                            int tiles, int jblocks, int64_t lo,
+                                                            int64_t hi, int H, int accumulate) {
+  static_assert(NT % D == 0, "a residue class needs whole thread runs");
+  constexpr int J = TT / D;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* G = reinterpret_cast<T*>(smem_raw);
+  constexpr int C = CPLX ? 2 : 1;
+  const int64_t dil = st.dil;
+  const int64_t row = blockIdx.x / tiles;
+  const int tile = (int)(blockIdx.x % tiles);
+  const int64_t R0 = (int64_t)(tile / jblocks) * D;
+  const int64_t j0 = (int64_t)(tile % jblocks) * J;
+  const int nel = D * (J + 2 * H) * C;
+  const int64_t qbase = lo - st.x_off + R0 + dil * (j0 - H);  // g position of element 0
+  const T* taps = static_cast<const T*>(st.taps);
+  const int tid = threadIdx.x;
+  T* gxrow = gx + row * st.n_in;
+  if (!accumulate) {  // zero the positions g does not reach, spread over the row's tiles
+    const int64_t outside = lo + (st.n_in - hi);
+    for (int64_t j = (int64_t)tile * NT + tid; j < outside; j += (int64_t)tiles * NT)
+      gxrow[j < lo ? j : hi + (j - lo)] = T(0);
+  }
+  T acc[RUN];
+#pragma unroll
+  for (int k = 0; k < RUN; ++k) acc[k] = T(0);
+  // g position of float element k of the tile (and its channel)
+  auto gpos = [&](int k) -> int64_t {
+    const int i = k / C;
+    return qbase + (i % D) + dil * (i / D);
+  };
+  constexpr int GPF = sizeof(T) == 8 ? 4 : 8;
+  T gr[GPF];
+  auto fetch = [&](int s) {
+    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out) * C;
+#pragma unroll
+    for (int e = 0; e < GPF; ++e) {
+      const int k = tid + e * NT;
+      if (e * NT < nel) {
+        const int64_t q = gpos(k);
+        gr[e] = grow[min(max(q, (int64_t)0), st.n_out - 1) * C + (k % C)];
+      }
+    }
+  };
+  const int r = tid % D, b = tid / D;
+  const int pb = adj_phys<D>(D * H + r + D * RUN * b);  // phys of U_0
+  if (st.n_scales > 0) fetch(0);
+  for (int s = 0; s < st.n_scales; ++s) {
+    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out) * C;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < GPF; ++e) {
+      const int k = tid + e * NT;
+      if (e * NT < nel && k < nel) {
+        const int64_t q = gpos(k);
+        G[adj_phys<D>(k / C) * C + (k % C)] = (q >= 0 && q < st.n_out) ? gr[e] : T(0);
+      }
+    }
+    for (int k = GPF * NT + tid; k < nel; k += NT) {
+      const int64_t q = gpos(k);
+      const T w = grow[min(max(q, (int64_t)0), st.n_out - 1) * C + (k % C)];
+      G[adj_phys<D>(k / C) * C + (k % C)] = (q >= 0 && q < st.n_out) ? w : T(0);
+    }
+    __syncthreads();
+    if (s + 1 < st.n_scales) fetch(s + 1);
+    const int tmax = st.sup[s];
+    const T* tp = taps + s * (st.half + 1) * C;
+    T upr[RUN], upi[RUN], dnr[RUN], dni[RUN];
+    {
+      const T h0 = tp[0];
+#pragma unroll
+      for (int k = 0; k < RUN; ++k) {
+        const T* e = G + (pb + D * k) * C;
+        upr[k] = dnr[k] = e[0];
+        if (CPLX) upi[k] = dni[k] = e[1];
+        acc[k] = fma(h0, upr[k], acc[k]);
+      }
+    }
+    for (int t0 = 1, blk = 0; t0 <= tmax; t0 += RUN, ++blk) {
+      const T* ub = G + (pb + D * (RUN + 1) * blk) * C;
+      const T* db = G + (pb - D * (RUN + 1) * blk) * C;
+#pragma unroll
+      for (int u = 0; u < RUN; ++u) {
+        if (t0 + u <= tmax) {
+          // U_{t-1+RUN} into up slot u, U_{-t} into down slot RUN-1-u (t = t0 + u)
+          const T* eu = ub + D * (u + RUN + 1) * C;
+          const T* ed = db - D * (u + 2) * C;
+          upr[u] = eu[0];
+          dnr[RUN - 1 - u] = ed[0];
+          if (CPLX) {
+            upi[u] = eu[1];
+            dni[RUN - 1 - u] = ed[1];
+          }
+          const T hr = tp[(t0 + u) * C];
+          const T hi_ = CPLX ? tp[(t0 + u) * C + 1] : T(0);
+#pragma unroll
+          for (int k = 0; k < RUN; ++k) {
+            const int a = (k + 1 + u) % RUN, c = (k + 2 * RUN - 1 - u) % RUN;
+            acc[k] = fma(hr, upr[a] + dnr[c], acc[k]);
+            if (CPLX) acc[k] = fma(hi_, upi[a] - dni[c], acc[k]);
+          }
+        }
+      }
+    }
+  }
+  if (R0 + r < dil) {
+#pragma unroll
+    for (int k = 0; k < RUN; ++k) {
+      const int64_t p = lo + R0 + r + dil * (j0 + RUN * b + k);
+      if (p < hi) gxrow[p] = accumulate ? gxrow[p] + acc[k] : acc[k];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ filter gradient
 // Partial sums per workgroup of  gh[s][k][ch] = sum_n g[s, n, ch] x[n + x_off - dil (k - half)]
 // for k = 0 .. 2 half (every tap, no symmetry assumed).  partial: (n_el, blocks) with
@@ -233,7 +382,7 @@ __global__ void __launch_bounds__(NT) morlet_backward_x_kernel(Stage st, const T
 // HS HB C sums of a lane are reduced over the 64 lanes of the wave by a butterfly that halves
 // the values per lane at every step (reduce-scatter), then written by the lanes that hold them.
 constexpr int HB = 8;   // taps per block
-constexpr int HS = 4;   // scales per group
+constexpr int HS4 = 4;  // scales per group (largest)
 constexpr int HP = 4;   // consecutive positions per lane and step
 constexpr int HPAD = 16;  // zeros in front of the x tile (window reads of clamped taps)
 
@@ -274,10 +423,13 @@ __device__ inline int butterfly_index(int lane) {
   return idx;
 }
 
-template <typename T, bool CPLX, int DIL>  // DIL: 1, 2, or 0 for any multiple of 4
+// One launch handles the scales [s_begin, s_end) in groups of HS (4, 2 or 1): the host
+// launches the last n_scales % 4 scales with a smaller HS, so no group computes empty scales.
+template <typename T, bool CPLX, int DIL, int HS>  // DIL: 1, 2, or 0 for any multiple of 4
 __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T* __restrict__ g,
                                                                T* __restrict__ partial,
-                                                               int g_scales, int tiles) {
+                                                               int g_scales, int tiles,
+                                                               int s_begin, int s_end) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int C = CPLX ? 2 : 1;
   constexpr int NV = HS * HB * C;  // sums per lane (a power of two)
@@ -296,8 +448,9 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
   const int K = 2 * half + 1;
   const int nvalid = (int)min((int64_t)TT, st.n_out - n0);
   typedef T v4 __attribute__((ext_vector_type(4)));
-  for (int s0 = 0; s0 < st.n_scales; s0 += HS) {
-    const int ns = min(HS, st.n_scales - s0);
+  const int nq = (nvalid + 64 * HP - 1) / (64 * HP);  // position steps holding valid g
+  for (int s0 = s_begin; s0 < s_end; s0 += HS) {
+    const int ns = min(HS, s_end - s0);
     __syncthreads();
     for (int k = tid; k < HS * TT * C; k += NT) {
       const int sl = k / (TT * C), r = k % (TT * C), i = r / C, ch = r % C;
@@ -315,7 +468,7 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
         for (int b = 0; b < HB; ++b)
 #pragma unroll
           for (int ch = 0; ch < C; ++ch) acc[a][b][ch] = T(0);
-      for (int q = 0; q < TT / (64 * HP); ++q) {
+      for (int q = 0; q < nq; ++q) {
         const int i = (q * 64 + lane) * HP;
         T gv[HS][C][HP];
 #pragma unroll
@@ -954,11 +1107,57 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
     if (chan[s] >= g_scales) return FDWT_ERR_ARG;
   if (rows == 0 || n_in == 0) return 0;
   if (n_out == 0) return FDWT_ERR_ARG;
-  const int tiles = (int)cdiv(n_in, TT);
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
+  {
+    // windowed kernel (power-of-two dilation): tiles over the range g reaches, with the
+    // residue-group size D that minimises a cost model of tap work plus staged elements
+    const int64_t reach = (int64_t)dil * half;
+    const int64_t lo = std::min(std::max(x_off - reach, (int64_t)0), n_in);
+    const int64_t hi = std::min(std::max(x_off + n_out + reach, lo), n_in);
+    const int H = (half + RUN - 1) / RUN * RUN;
+    const int64_t nj = std::max((int64_t)1, cdiv(hi - lo, dil));
+    int best_d = 0;
+    int64_t best_tiles = 0, best_jb = 0;
+    double best_cost = 0;
+    for (int d = 1; d <= 64 && d <= dil; d *= 2) {
+      const int64_t J = TT / d;
+      const int64_t jb = cdiv(nj, J);
+      const int64_t tl = (dil / d) * jb;
+      const size_t lds = (size_t)(d * (J + 2 * H) * (RUN + 1) / RUN + d) * channels * cs;
+      if (lds > 160 * 1024 || tl > INT32_MAX) continue;
+      const double cost = (double)tl * ((double)TT * (2 * half + 1) + 48.0 * d * (J + 2 * H)) *
+                          channels;
+      if (!best_d || cost < best_cost) best_d = d, best_cost = cost, best_tiles = tl, best_jb = jb;
+    }
+    if ((dil & (dil - 1)) == 0 && best_d) {
+      const int64_t J = TT / best_d;
+      const size_t lds =
+          (size_t)(best_d * (J + 2 * H) * (RUN + 1) / RUN + best_d) * channels * cs;
+#define ADJ(TYPE, CPLX, DD)                                                                  \
+  case DD: {                                                                                 \
+    auto k = morlet_adjoint_kernel<TYPE, CPLX, DD>;                                          \
+    FDWT_LDS_ONCE(k);                                                                        \
+    return launch(k, rows * best_tiles, lds, hs, st, (const TYPE*)g, (TYPE*)gx,               \
+                  (int)g_scales, (int)best_tiles, (int)best_jb, lo, hi, H, (int)accumulate);  \
+  }
+#define ADJ_ALL(TYPE, CPLX)                                                                  \
+  switch (best_d) {                                                                          \
+    ADJ(TYPE, CPLX, 1) ADJ(TYPE, CPLX, 2) ADJ(TYPE, CPLX, 4) ADJ(TYPE, CPLX, 8)              \
+    ADJ(TYPE, CPLX, 16) ADJ(TYPE, CPLX, 32) ADJ(TYPE, CPLX, 64) default: break;              \
+  }
+      if (dtype == FDWT_F32) {
+        if (channels == 2) ADJ_ALL(float, true) else ADJ_ALL(float, false)
+      } else {
+        if (channels == 2) ADJ_ALL(double, true) else ADJ_ALL(double, false)
+      }
+#undef ADJ_ALL
+#undef ADJ
+    }
+  }
+  const int tiles = (int)cdiv(n_in, TT);
   const size_t lds = (size_t)((TT + 2 * (int64_t)dil * half) * channels + 4) * cs;
-#define BWX(TYPE, CPLX)                                                                     \
+#define BWX(TYPE, CPLX)                                                                    \
   do {                                                                                      \
     auto k = morlet_backward_x_kernel<TYPE, CPLX>;                                          \
     FDWT_LDS_ONCE(k);                                                                       \
@@ -1002,17 +1201,28 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
   const int64_t span = TT + 2 * (int64_t)dil * half;
-  const size_t lds = (size_t)(HPAD + ((span + 4 + 3) & ~3) + (int64_t)HS * TT * channels) * cs;
+  const size_t lds = (size_t)(HPAD + ((span + 4 + 3) & ~3) + (int64_t)HS4 * TT * channels) * cs;
   const int64_t blocks = rows * tiles;
   if (n_el > INT32_MAX) return FDWT_ERR_ARG;
   if (dil != 1 && dil != 2 && dil % 4 != 0) return FDWT_ERR_ARG;
-  int rc;
-#define BWH_DIL(TYPE, CPLX, D)                                                                \
+  // scales [0, n4) in groups of 4; the remaining 1 or 2 in one smaller group (3 stay in a
+  // group of 4, one slot idle)
+  const int rem = n_scales % 4;
+  const int n4 = rem == 3 ? n_scales : n_scales - rem;
+  int rc = 0;
+#define BWH_HS(TYPE, CPLX, D, S, B, E)                                                        \
   do {                                                                                        \
-    auto k = morlet_backward_h_kernel<TYPE, CPLX, D>;                                         \
+    auto k = morlet_backward_h_kernel<TYPE, CPLX, D, S>;                                      \
     FDWT_LDS_ONCE(k);                                                                         \
     rc = launch(k, blocks, lds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,      \
-                tiles);                                                                       \
+                tiles, (int)(B), (int)(E));                                                   \
+  } while (0)
+#define BWH_DIL(TYPE, CPLX, D)                                                                \
+  do {                                                                                        \
+    if (n4 > 0) BWH_HS(TYPE, CPLX, D, 4, 0, n4);                                              \
+    if (rc) return rc;                                                                        \
+    if (n4 < n_scales && n_scales - n4 == 1) BWH_HS(TYPE, CPLX, D, 1, n4, n_scales);          \
+    if (n4 < n_scales && n_scales - n4 == 2) BWH_HS(TYPE, CPLX, D, 2, n4, n_scales);          \
   } while (0)
 #define BWH(TYPE, CPLX)                                                                       \
   do {                                                                                        \
@@ -1031,6 +1241,7 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   BWH(double, false);
 #undef BWH
 #undef BWH_DIL
+#undef BWH_HS
 }
 
 extern "C" int64_t fdwt_mix_workspace(int64_t rows, int64_t n_out, int32_t n_scales) {
