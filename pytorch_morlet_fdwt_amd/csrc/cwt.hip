@@ -1111,7 +1111,11 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
   const int cs = dtype == FDWT_F64 ? 8 : 4;
   {
     // windowed kernel (power-of-two dilation): tiles over the range g reaches, with the
-    // residue-group size D that minimises a cost model of tap work plus staged elements
+    // residue-group size D that minimises a cost model of tap work plus staged elements.
+    // D >= min(dil, 4): below that the staging gathers runs of 1-2 complex values with
+    // stride dil, a cache line per value (on MI355X such tiles ran up to 2x slower than the
+    // model predicts; the weight 48 and this floor come from timing every D on the octaves
+    // of the CWT, TokenMixer and attention configurations).
     const int64_t reach = (int64_t)dil * half;
     const int64_t lo = std::min(std::max(x_off - reach, (int64_t)0), n_in);
     const int64_t hi = std::min(std::max(x_off + n_out + reach, lo), n_in);
@@ -1120,7 +1124,7 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
     int best_d = 0;
     int64_t best_tiles = 0, best_jb = 0;
     double best_cost = 0;
-    for (int d = 1; d <= 64 && d <= dil; d *= 2) {
+    for (int d = std::min(dil, 4); d <= 64 && d <= dil; d *= 2) {
       const int64_t J = TT / d;
       const int64_t jb = cdiv(nj, J);
       const int64_t tl = (dil / d) * jb;
