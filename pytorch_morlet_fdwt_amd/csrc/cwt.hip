@@ -534,6 +534,177 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
   }
 }
 
+// ------------------------------------------------------------------ filter gradient, MFMA
+// The same partial sums as a matrix product on the matrix cores:
+//     gh[(s, ch)][k] = sum_n G[(s, ch)][n] X[n][k],   X[n][k] = x[n + x_off - dil (k - half)]
+// with one v_mfma_*_16x16x4 per 4 positions and 16 taps: A = G (16 rows = up to 16 / C
+// scales x C channels, 4 positions), B = X (4 positions x 16 taps), accumulated in the
+// instruction's 16 x 16 result for every tap block of the stage (K <= 16 MB_KB).
+// Operand layout (16x16x4, one block): lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
+// result element e of lane l is D[row][l % 16] with row = 4 (l / 16) + e for f32 and
+// (l / 16) + 4 e for f64 (both measured on gfx950).
+//
+// A workgroup loops over position tiles (row, n0) with stride gridDim.x, so the sums stay in
+// the result registers over several tiles; each wave takes a quarter of every tile.  G comes
+// straight from global memory (each element is read once); the x tile (TT + 2 dil half + 4
+// samples) is staged in LDS with one word of skew per min(dil, 64) words (dil >= 8), so the
+// 16 taps of an instruction (addresses dil apart) fall in distinct banks.  At the end the four waves' sums are added in
+// LDS and the workgroup writes column blockIdx.x of `partial` (n_el x gridDim.x).
+constexpr int MB_KB = 8;   // tap blocks of 16 (K <= 128)
+constexpr int MB_U = 16;   // instructions per A prefetch chunk (TT / 4 is a multiple of 4 MB_U)
+constexpr int MB_XR = 1;   // x window registers per thread (the first MB_XR NT samples)
+
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<float> {
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  static __device__ inline v4 mma(float a, float b, v4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline int row(int lane, int e) { return 4 * (lane / 16) + e; }
+};
+template <>
+struct Mfma16<double> {
+  typedef double v4 __attribute__((ext_vector_type(4)));
+  static __device__ inline v4 mma(double a, double b, v4 c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline int row(int lane, int e) { return lane / 16 + 4 * e; }
+};
+
+template <typename T, bool CPLX, int KB>  // KB = ceil(K / 16) tap blocks
+__global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const T* __restrict__ g,
+                                                                T* __restrict__ partial,
+                                                                int g_scales, int tiles,
+                                                                int64_t total, int s_begin,
+                                                                int s_end, int sk) {
+  constexpr int kblocks = KB;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  typedef typename Mfma16<T>::v4 v4;
+  constexpr int C = CPLX ? 2 : 1;
+  T* const X = reinterpret_cast<T*>(smem_raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = st.half, dil = st.dil, K = 2 * half + 1;
+  const int span = TT + 2 * dil * half + 4;
+  const int ns = s_end - s_begin;
+  const int arow = lane & 15, asl = arow / C, ach = arow % C;
+  const bool arow_ok = asl < ns;
+  const int chan_a = arow_ok ? st.chan[s_begin + asl] : 0;
+  const int kpos = lane >> 4;  // position of this lane within an instruction's four
+  // skewed LDS index of x element i: i + (i >> sk), 2^sk = min(dil, 64) (no skew below
+  // dil 8).  Tap offsets are multiples of 2^sk, so skew(p + off) = skew(p) + skew(off).
+  auto skew = [sk](int i) { return i + (i >> sk); };
+  int boff[KB];                // skewed x offset of this lane's tap in every block
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) boff[kb] = skew(dil * (2 * half - min(kb * 16 + arow, K - 1)));
+  v4 acc[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) acc[kb] = v4{T(0), T(0), T(0), T(0)};
+  // Software pipeline over the workgroup's tiles: the x window of the next tile is loaded into
+  // registers (its first MB_XR NT samples) while the current tile is multiplied, and the last
+  // A chunk of a tile is followed by the first chunk of the next tile.  Loads are unconditional
+  // from clamped (valid) indices; masks are applied where the values are used.
+  const int pbeg = wave * (TT / 4);
+  struct Tile {
+    const T* grow;  // g of this lane's A row at the tile's first position
+    const T* xrow;
+    int64_t xb;     // x index of window element 0
+    int nvalid;
+  };
+  auto tile_of = [&](int64_t t) {
+    Tile q;
+    const int64_t row = t / tiles, n0 = (t % tiles) * (int64_t)TT;
+    q.grow = g + ((row * g_scales + chan_a) * st.n_out + n0) * C + ach;
+    q.xrow = static_cast<const T*>(st.x) + row * st.n_in;
+    q.xb = n0 + st.x_off - (int64_t)dil * half;
+    q.nvalid = (int)min((int64_t)TT, st.n_out - n0);
+    return q;
+  };
+  T an[MB_U], xr[MB_XR];
+  auto load_a = [&](const Tile& q, int c0) {
+#pragma unroll
+    for (int u = 0; u < MB_U; ++u) an[u] = q.grow[(int64_t)min(c0 + 4 * u + kpos, q.nvalid - 1) * C];
+  };
+  auto load_x = [&](const Tile& q) {
+#pragma unroll
+    for (int r = 0; r < MB_XR; ++r)
+      xr[r] = q.xrow[min(max(q.xb + tid + r * NT, (int64_t)0), st.n_in - 1)];
+  };
+  int64_t t = blockIdx.x;
+  Tile cur_t = tile_of(t < total ? t : 0);
+  load_x(cur_t);
+  load_a(cur_t, pbeg);
+  for (; t < total; t += gridDim.x) {
+    const Tile nxt = tile_of(t + gridDim.x < total ? t + gridDim.x : t);
+    __syncthreads();  // the previous tile's reads of X are done
+#pragma unroll
+    for (int r = 0; r < MB_XR; ++r) {
+      const int i = tid + r * NT;
+      const int64_t xi = cur_t.xb + i;
+      if (i < span) X[skew(i)] = (xi >= 0 && xi < st.n_in) ? xr[r] : T(0);
+    }
+    for (int i = tid + MB_XR * NT; i < span; i += NT)
+      X[skew(i)] = load_clamped(cur_t.xrow, cur_t.xb + i, st.n_in);
+    __syncthreads();
+    load_x(nxt);
+    const int nvalid = cur_t.nvalid;
+    const int pend = min(pbeg + TT / 4, nvalid);
+    if (pbeg >= pend) load_a(nxt, pbeg);  // no positions of this tile for this wave
+    for (int c0 = pbeg; c0 < pend; c0 += 4 * MB_U) {
+      T cur[MB_U];
+#pragma unroll
+      for (int u = 0; u < MB_U; ++u)
+        cur[u] = (arow_ok && c0 + 4 * u + kpos < nvalid) ? an[u] : T(0);
+      const bool last = c0 + 4 * MB_U >= pend;
+      load_a(last ? nxt : cur_t, last ? pbeg : c0 + 4 * MB_U);
+      // B values: the LDS reads of step u + 1 are issued before the instructions of step u,
+      // so an instruction never waits for its own read (fences keep that order; without them
+      // the compiler reuses one register and puts a full LDS wait before every instruction)
+      T bc[KB], bn[KB];
+      {
+        const T* xp = X + skew(c0 + kpos);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) bc[kb] = xp[boff[kb]];
+      }
+#pragma unroll
+      for (int u = 0; u < MB_U; ++u) {
+        if (u + 1 < MB_U) {
+          const T* xp = X + skew(c0 + 4 * (u + 1) + kpos);
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) bn[kb] = xp[boff[kb]];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) acc[kb] = Mfma16<T>::mma(cur[u], bc[kb], acc[kb]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) bc[kb] = bn[kb];
+      }
+    }
+    cur_t = nxt;
+  }
+  // add the four waves' sums (X is free now) and write this workgroup's column
+  __syncthreads();
+  T* const red = X;  // [wave][kb][e][lane]
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[((wave * kblocks + kb) * 4 + e) * 64 + lane] = acc[kb][e];
+  }
+  __syncthreads();
+  const int64_t ncols = gridDim.x;
+  for (int idx = tid; idx < kblocks * 256; idx += NT) {
+    T v = T(0);
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) v += red[w * kblocks * 256 + idx];
+    const int kb = idx / 256, e = (idx / 64) % 4, l = idx % 64;
+    const int i = Mfma16<T>::row(l, e), sl = i / C, ch = i % C, k = kb * 16 + (l % 16);
+    if (sl < ns && k < K)
+      partial[((int64_t)((s_begin + sl) * K + k) * C + ch) * ncols + blockIdx.x] = v;
+  }
+}
+
 // ------------------------------------------------------------------ half-band chain step
 // y[n] (+)= t0 x[n + b] + sum_{t odd <= c} taps[t] (x[n + b - dil t] + x[n + b + dil t])
 template <typename T>
@@ -1016,6 +1187,20 @@ inline bool allow_full_lds(K kernel) {
   return true;
 }
 
+// Workgroups of `kernel` (NT threads, `lds` bytes) resident on the whole device at once,
+// at most `cap` (a persistent grid: one round of workgroups).
+template <typename K>
+inline int resident_blocks(K kernel, size_t lds, int64_t cap) {
+  int dev = 0, per_cu = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                   NT, lds) != hipSuccess)
+    per_cu = 1, cus = 256;
+  const int64_t n = (int64_t)std::max(per_cu, 1) * std::max(cus, 1);
+  return (int)std::max<int64_t>(1, std::min(n, cap));
+}
+
 template <typename K, typename... Args>
 int launch(K kernel, int64_t blocks, size_t lds, hipStream_t st, Args... args) {
   if (blocks <= 0) return 0;
@@ -1205,6 +1390,45 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
   const int64_t span = TT + 2 * (int64_t)dil * half;
+  if (K <= 16 * MB_KB && rows * tiles <= INT32_MAX) {
+    // matrix-core path: launches over groups of 16 / C scales, then one column reduction
+    const int64_t total = rows * tiles;
+    const int kblocks = (int)cdiv(K, 16);
+    const int sk = (dil < 8 || (dil & (dil - 1))) ? 30 : (dil >= 64 ? 6 : __builtin_ctz(dil));
+    const int64_t xs = (span + 4 - 1) + ((span + 4 - 1) >> sk) + 1;
+    const size_t mlds = (size_t)std::max<int64_t>(xs, (int64_t)(NT / 64) * kblocks * 256) * cs;
+    const int grp = 16 / channels;
+    int rc = 0, ncols = 1;
+#define GHM_KB(TYPE, CPLX, N)                                                                 \
+  case N: {                                                                                   \
+    auto k = morlet_grad_h_mfma_kernel<TYPE, CPLX, N>;                                        \
+    FDWT_LDS_ONCE(k);                                                                         \
+    ncols = resident_blocks(k, mlds, total);                                                  \
+    for (int s0 = 0; s0 < n_scales && !rc; s0 += grp)                                         \
+      rc = launch(k, ncols, mlds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,    \
+                  tiles, total, s0, std::min(n_scales, s0 + grp), sk);                        \
+    break;                                                                                    \
+  }
+#define GHM(TYPE, CPLX)                                                                       \
+  do {                                                                                        \
+    switch (kblocks) {                                                                        \
+      GHM_KB(TYPE, CPLX, 1) GHM_KB(TYPE, CPLX, 2) GHM_KB(TYPE, CPLX, 3)                       \
+      GHM_KB(TYPE, CPLX, 4) GHM_KB(TYPE, CPLX, 5) GHM_KB(TYPE, CPLX, 6)                       \
+      GHM_KB(TYPE, CPLX, 7) GHM_KB(TYPE, CPLX, 8) default: return FDWT_ERR_ARG;               \
+    }                                                                                         \
+    if (rc) return rc;                                                                        \
+    return launch(reduce_cols_kernel<TYPE>, n_el, 0, hs, (const TYPE*)workspace, (TYPE*)gh,   \
+                  (int64_t)ncols, (int)accumulate);                                           \
+  } while (0)
+    if (dtype == FDWT_F32) {
+      if (channels == 2) GHM(float, true);
+      GHM(float, false);
+    }
+    if (channels == 2) GHM(double, true);
+    GHM(double, false);
+#undef GHM
+#undef GHM_KB
+  }
   const size_t lds = (size_t)(HPAD + ((span + 4 + 3) & ~3) + (int64_t)HS4 * TT * channels) * cs;
   const int64_t blocks = rows * tiles;
   if (n_el > INT32_MAX) return FDWT_ERR_ARG;
