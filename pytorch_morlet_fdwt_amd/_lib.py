@@ -128,6 +128,10 @@ def set_timer(timer):
 def launch(name: str, device, *args):
     """Call entry point ``name`` with ``args`` on ``device`` and raise on failure."""
     fn = getattr(lib(), name)
+    idx = device.index if isinstance(device, torch.device) else device
+    if _TIMER is None and (idx is None or idx == torch.cuda.current_device()):
+        check(fn(*args), name)  # already the current device: no device switch
+        return
     with torch.cuda.device(device):
         if _TIMER is None:
             check(fn(*args), name)

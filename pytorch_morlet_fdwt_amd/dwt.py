@@ -14,6 +14,8 @@ Every forward and backward is a hand-written HIP kernel (``csrc/dwt.hip``):
 
 from __future__ import annotations
 
+import functools
+
 from typing import List, Optional, Sequence, Tuple
 
 import torch
@@ -67,8 +69,13 @@ def _synthesis(a2, d2, h0, h1, mode, off, n, R, dtype, device):
     return y
 
 
+@functools.lru_cache(maxsize=None)
+def _chain_max(taps: int, dtype) -> int:
+    return _lib.lib().fdwt_chain_max_length(taps, _lib.dtype_code(dtype))
+
+
 def _chain_fits(n: int, taps: int, dtype) -> bool:
-    return n <= _lib.lib().fdwt_chain_max_length(taps, _lib.dtype_code(dtype))
+    return n <= _chain_max(taps, dtype)
 
 
 def _analysis_chain(x2, h0, h1, mode, off, n_in, n_out):
@@ -184,15 +191,20 @@ class _AnalysisChain(torch.autograd.Function):
     Backward is :class:`_SynthesisChain` with the transposed level parameters."""
 
     @staticmethod
-    def forward(ctx, x, h0, h1, mode: int, off: int, n_in: tuple, n_out: tuple):
+    def run(x, h0, h1, mode: int, off: int, n_in: tuple, n_out: tuple):
+        """The transform itself (no autograd node)."""
         _lib.require_gpu(x)
-        ctx.save_for_backward(h0, h1)
-        ctx.cfg = (mode, off, n_in, n_out)
         lead = x.shape[:-1]
         details, approx = _analysis_chain(_rows(x), h0, h1, mode, off, n_in, n_out)
         outs = [d.reshape(*lead, d.shape[-1]) for d in details]
         outs.append(approx.reshape(*lead, approx.shape[-1]))
         return tuple(outs)
+
+    @staticmethod
+    def forward(ctx, x, h0, h1, mode: int, off: int, n_in: tuple, n_out: tuple):
+        ctx.save_for_backward(h0, h1)
+        ctx.cfg = (mode, off, n_in, n_out)
+        return _AnalysisChain.run(x, h0, h1, mode, off, n_in, n_out)
 
     @staticmethod
     def backward(ctx, *grads):
@@ -201,9 +213,11 @@ class _AnalysisChain(torch.autograd.Function):
         if not ctx.needs_input_grad[0]:
             return (None,) * 7
         gd, ga = list(grads[:-1]), grads[-1]
-        # transpose: coarsest level first; nc = n_out[l], output length = n_in[l]
-        gx = _SynthesisChain.apply(h0, h1, mode, off, tuple(n_out[::-1]), tuple(n_in[::-1]),
-                                   ga, *gd[::-1])
+        # transpose: coarsest level first; nc = n_out[l], output length = n_in[l].  A graph
+        # node only when the backward itself is differentiated (create_graph=True)
+        args = (h0, h1, mode, off, tuple(n_out[::-1]), tuple(n_in[::-1]), ga, *gd[::-1])
+        gx = (_SynthesisChain.apply(*args) if torch.is_grad_enabled()
+              else _SynthesisChain.run(*args))
         return gx, None, None, None, None, None, None
 
 
@@ -214,11 +228,16 @@ class _SynthesisChain(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h0, h1, mode: int, off: int, nc: tuple, n_out: tuple, a, *ds):
-        ref = a if a is not None else next(d for d in ds if d is not None)
-        _lib.require_gpu(a, *ds)
         ctx.save_for_backward(h0, h1)
         ctx.cfg = (mode, off, nc, n_out)
         ctx.n_ds = len(ds)
+        return _SynthesisChain.run(h0, h1, mode, off, nc, n_out, a, *ds)
+
+    @staticmethod
+    def run(h0, h1, mode: int, off: int, nc: tuple, n_out: tuple, a, *ds):
+        """The transform itself (no autograd node)."""
+        ref = a if a is not None else next(d for d in ds if d is not None)
+        _lib.require_gpu(a, *ds)
         lead = ref.shape[:-1]
         R = 1
         for s in lead:
@@ -234,7 +253,9 @@ class _SynthesisChain(torch.autograd.Function):
         mode, off, nc, n_out = ctx.cfg
         if not any(ctx.needs_input_grad[6:]):
             return (None,) * (7 + ctx.n_ds)
-        outs = _AnalysisChain.apply(gy, h0, h1, mode, off, tuple(n_out[::-1]), tuple(nc[::-1]))
+        args = (gy, h0, h1, mode, off, tuple(n_out[::-1]), tuple(nc[::-1]))
+        outs = (_AnalysisChain.apply(*args) if torch.is_grad_enabled()
+                else _AnalysisChain.run(*args))
         gds = list(outs[:-1])[::-1]  # coarsest first
         return (None,) * 6 + (outs[-1],) + tuple(gds)
 
