@@ -544,9 +544,9 @@ def main():
     if not a.no_legs:
         cpu = not a.no_cpu_baseline
         k = max(3, a.steps // 2)
-        line["dwt_cfg1"] = dwt_cfg1(k, a.warmup, dev, cpu)
         line["cwt_cfg3"] = cwt_cfg3(k, a.warmup, dev, cpu)
         line["token_mixer_cfg4"] = token_mixer_cfg4(k, a.warmup, dev, cpu)
+        line["dwt_cfg1"] = dwt_cfg1(k, a.warmup, dev, cpu)
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(a.cpu_rows)
     print(json.dumps(line))
