@@ -342,11 +342,12 @@ class _MorletCWTFunction(torch.autograd.Function):
         H = H.to(x.dtype)
         xs = [x]
         by_oct = {st.octave: k for k, st in enumerate(plan.stages)}
+        tables = {}
         for j in range(plan.n_octaves):
             if j in by_oct:
                 k = by_oct[j]
                 st, sup, chan, _ = _stage_args(plan, k)
-                taps = plan.stage_taps(H, k)
+                taps = tables[k] = plan.stage_taps(H, k)
                 _lib.launch("fdwt_morlet_forward", x.device, _lib.ptr(xs[j]), _lib.ptr(taps),
                             _lib.ptr(y), R, xs[j].shape[1], N, plan.margins[j],
                             len(st.scale_idx), st.half, sup, chan, st.dil, C, plan.num_scales,
@@ -357,6 +358,7 @@ class _MorletCWTFunction(torch.autograd.Function):
         ctx.x_dtype = x.dtype
         ctx.need_h = need_h
         ctx.n_x = len(xs) if need_h else 0
+        ctx.tables = tables
         ctx.save_for_backward(*(xs if need_h else []), H)
         return y
 
@@ -381,7 +383,7 @@ class _MorletCWTFunction(torch.autograd.Function):
             if j in by_oct:
                 k = by_oct[j]
                 st, sup, chan, _ = _stage_args(plan, k)
-                taps = plan.stage_taps(H, k)
+                taps = ctx.tables[k]  # the forward's compact tap tables
                 gh = _stage_backward(plan, k, xs[j] if ctx.need_h else None, g, plan.num_scales,
                                      chan, taps, gx, filled, ctx.need_h)
                 filled = True
@@ -419,12 +421,13 @@ class _MorletMixFunction(torch.autograd.Function):
         y = torch.empty((R, N), device=x.device, dtype=dt)
         xs = [x]
         by_oct = {st.octave: k for k, st in enumerate(plan.stages)}
+        tables = {}
         first = True
         for j in range(plan.n_octaves):
             if j in by_oct:
                 k = by_oct[j]
                 st, sup, chan, _ = _stage_args(plan, k)
-                taps = plan.stage_taps(H, k)
+                taps = tables[k] = plan.stage_taps(H, k)
                 _lib.launch("fdwt_mix_forward", x.device, _lib.ptr(xs[j]), _lib.ptr(taps),
                             _lib.ptr(a_), _lib.ptr(b_), _lib.ptr(y), R, xs[j].shape[1], N,
                             plan.margins[j], len(st.scale_idx), st.half, sup, chan, st.dil,
@@ -437,6 +440,7 @@ class _MorletMixFunction(torch.autograd.Function):
             y.zero_()
         ctx.plan = plan
         ctx.x_dtype = x.dtype
+        ctx.tables = tables
         ctx.save_for_backward(*xs, H, a_, b_)
         ctx.n_x = len(xs)
         return y
@@ -472,7 +476,7 @@ class _MorletMixFunction(torch.autograd.Function):
                 k = by_oct[j]
                 st, sup, chan, local = _stage_args(plan, k)
                 S_j = len(st.scale_idx)
-                taps = plan.stage_taps(H, k)
+                taps = ctx.tables[k]  # the forward's compact tap tables
                 chunk = max(1, _MorletMixFunction.MIX_CHUNK_BYTES // (S_j * N * C * gy.element_size()))
                 gh_acc = None
                 for r0, r1 in _stage_chunks(R, chunk, D):
@@ -542,12 +546,13 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
         out = torch.empty_like(m)
         by_oct = {st.octave: k for k, st in enumerate(plan.stages)}
         last_j = max(by_oct)
+        tables = {}
         xj = x
         for j in range(plan.n_octaves):
             if j in by_oct:
                 k = by_oct[j]
                 st, sup, chan, _ = _stage_args(plan, k)
-                taps = plan.stage_taps(H, k)
+                taps = tables[k] = plan.stage_taps(H, k)
                 _lib.launch("fdwt_softmax_forward", x.device, _lib.ptr(xj), _lib.ptr(taps),
                             _lib.ptr(V_), int(v_pos), V_.shape[1], nch, _lib.ptr(m), _lib.ptr(l),
                             _lib.ptr(out), R, xj.shape[1], N, plan.margins[j],
@@ -558,6 +563,7 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
                 xj = _lowpass_step(plan, xj, j, N)
         ctx.plan, ctx.nch, ctx.tau = plan, nch, tau
         ctx.x_dtype, ctx.v_dtype = x.dtype, V.dtype
+        ctx.tables = tables
         ctx.save_for_backward(x, H, V_, m, l, out)
         return out
 
@@ -589,7 +595,7 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
                 k = by_oct[j]
                 st, sup, chan, local = _stage_args(plan, k)
                 S_j = len(st.scale_idx)
-                taps = plan.stage_taps(H, k)
+                taps = ctx.tables[k]  # the forward's compact tap tables
                 idx = plan._index(k, dev)
                 chunk = max(1, _SpectralSoftmaxFunction.CHUNK_BYTES // (S_j * N * 2 * gy.element_size()))
                 gh_acc = None
