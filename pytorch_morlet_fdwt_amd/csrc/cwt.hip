@@ -547,8 +547,8 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
 // A workgroup loops over position tiles (row, n0) with stride gridDim.x, so the sums stay in
 // the result registers over several tiles; each wave takes a quarter of every tile.  G comes
 // straight from global memory (each element is read once); the x tile (TT + 2 dil half + 4
-// samples) is staged in LDS with one word of skew per min(dil, 64) words (dil >= 8), so the
-// 16 taps of an instruction (addresses dil apart) fall in distinct banks.  At the end the four waves' sums are added in
+// samples) is staged in LDS with four words of skew per dil words (dil >= 8), so the 16 taps
+// of an instruction (addresses dil apart) fall in distinct banks.  At the end the four waves' sums are added in
 // LDS and the workgroup writes column blockIdx.x of `partial` (n_el x gridDim.x).
 constexpr int MB_KB = 8;   // tap blocks of 16 (K <= 128)
 constexpr int MB_U = 16;   // instructions per A prefetch chunk (TT / 4 is a multiple of 4 MB_U)
@@ -592,9 +592,11 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
   const bool arow_ok = asl < ns;
   const int chan_a = arow_ok ? st.chan[s_begin + asl] : 0;
   const int kpos = lane >> 4;  // position of this lane within an instruction's four
-  // skewed LDS index of x element i: i + (i >> sk), 2^sk = min(dil, 64) (no skew below
-  // dil 8).  Tap offsets are multiples of 2^sk, so skew(p + off) = skew(p) + skew(off).
-  auto skew = [sk](int i) { return i + (i >> sk); };
+  // skewed LDS index of x element i: i + 4 (i >> sk) with 2^sk = dil (no skew below dil 8).
+  // Tap offsets are multiples of dil, so skew(p + off) = skew(p) + skew(off); consecutive taps
+  // are dil + 4 words apart, i.e. 4 banks (mod 64) for every power-of-two dil, so the 16 taps
+  // x 4 positions of an instruction's B operand fall in 64 distinct banks.
+  auto skew = [sk](int i) { return i + ((i >> sk) << 2); };
   int boff[KB];                // skewed x offset of this lane's tap in every block
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) boff[kb] = skew(dil * (2 * half - min(kb * 16 + arow, K - 1)));
@@ -1394,8 +1396,8 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
     // matrix-core path: launches over groups of 16 / C scales, then one column reduction
     const int64_t total = rows * tiles;
     const int kblocks = (int)cdiv(K, 16);
-    const int sk = (dil < 8 || (dil & (dil - 1))) ? 30 : (dil >= 64 ? 6 : __builtin_ctz(dil));
-    const int64_t xs = (span + 4 - 1) + ((span + 4 - 1) >> sk) + 1;
+    const int sk = (dil < 8 || (dil & (dil - 1))) ? 30 : __builtin_ctz(dil);
+    const int64_t xs = (span + 4 - 1) + 4 * ((span + 4 - 1) >> sk) + 1;
     const size_t mlds = (size_t)std::max<int64_t>(xs, (int64_t)(NT / 64) * kblocks * 256) * cs;
     const int grp = 16 / channels;
     int rc = 0, ncols = 1;
