@@ -46,6 +46,12 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
     return t.reshape(-1, t.shape[-1]).contiguous()
 
 
+def _contig(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """The entry points take a data pointer and a row count: any contiguous layout of the rows
+    will do, so only a non-contiguous tensor is copied (no reshape on the hot path)."""
+    return t if t is None or t.is_contiguous() else t.contiguous()
+
+
 # ----------------------------------------------------------------------------- launches
 def _analysis(x2, h0, h1, mode, off, n_out):
     R, n = x2.shape
@@ -78,16 +84,19 @@ def _chain_fits(n: int, taps: int, dtype) -> bool:
     return n <= _chain_max(taps, dtype)
 
 
-def _analysis_chain(x2, h0, h1, mode, off, n_in, n_out):
-    """Levels l = 0..J-1 of an analysis chain on x2 (R, n_in[0]).  Returns (details, approx).
-    Rows too long for LDS run their first levels one at a time."""
-    R = x2.shape[0]
+def _analysis_chain(x2, h0, h1, mode, off, n_in, n_out, lead=None):
+    """Levels l = 0..J-1 of an analysis chain on the contiguous rows of x2 (any shape
+    (*lead, n_in[0])).  Returns (details, approx), shaped (*lead, n) when the whole chain is one
+    launch (2-D (R, n) otherwise).  Rows too long for LDS run their first levels one at a time."""
+    lead = tuple(x2.shape[:-1]) if lead is None else lead
+    R = x2.numel() // x2.shape[-1] if x2.shape[-1] else 0
     J = len(n_in)
     taps = h0.numel()
     details = [None] * J
     l = 0
     cur = x2
     while l < J and J - l > 1 and not _chain_fits(n_in[l], taps, x2.dtype):
+        cur = cur.reshape(R, cur.shape[-1])
         if cur.shape[-1] < n_in[l]:
             cur = torch.nn.functional.pad(cur, (0, n_in[l] - cur.shape[-1]))
         cur, details[l] = _analysis(cur, h0, h1, mode, off, n_out[l])
@@ -95,8 +104,10 @@ def _analysis_chain(x2, h0, h1, mode, off, n_in, n_out):
     if l < J:
         if cur.shape[-1] < n_in[l]:
             cur = torch.nn.functional.pad(cur, (0, n_in[l] - cur.shape[-1]))
-        outs = [torch.empty((R, n_out[k]), device=x2.device, dtype=x2.dtype) for k in range(l, J)]
-        approx = torch.empty((R, n_out[J - 1]), device=x2.device, dtype=x2.dtype)
+        shp = lead if l == 0 else (R,)
+        outs = [torch.empty((*shp, n_out[k]), device=x2.device, dtype=x2.dtype)
+                for k in range(l, J)]
+        approx = torch.empty((*shp, n_out[J - 1]), device=x2.device, dtype=x2.dtype)
         if R:
             _lib.launch("fdwt_analysis_chain", x2.device,
                         _lib.ptr(cur), _lib.ptr_array(outs), _lib.ptr(approx), _lib.ptr(h0),
@@ -108,8 +119,10 @@ def _analysis_chain(x2, h0, h1, mode, off, n_in, n_out):
     return details, cur
 
 
-def _synthesis_chain(a2, ds, h0, h1, mode, off, nc, n_out, R, dtype, device):
-    """Levels k = 0..K-1 (coarsest first) of a synthesis chain.  a2 / ds[k] may be None."""
+def _synthesis_chain(a2, ds, h0, h1, mode, off, nc, n_out, R, dtype, device, lead=None):
+    """Levels k = 0..K-1 (coarsest first) of a synthesis chain on contiguous bands (any shape
+    with R rows).  a2 / ds[k] may be None.  The output is shaped (*lead, n_out[-1]) when the
+    last level runs in the chain (2-D (R, n) otherwise, or when lead is None)."""
     K = len(nc)
     taps = h0.numel()
     # the chain keeps every output but the last on chip: run it while that fits, then the
@@ -123,7 +136,8 @@ def _synthesis_chain(a2, ds, h0, h1, mode, off, nc, n_out, R, dtype, device):
     for g0 in range(0, k_end, _SYN_MAX_LEVELS):
         g1 = min(k_end, g0 + _SYN_MAX_LEVELS)
         a_in = a2 if g0 == 0 else cur[:, :nc[g0]].contiguous()
-        cur = torch.empty((R, n_out[g1 - 1]), device=device, dtype=dtype)
+        shp = lead if (lead is not None and g1 == K) else (R,)
+        cur = torch.empty((*shp, n_out[g1 - 1]), device=device, dtype=dtype)
         if R:
             _lib.launch("fdwt_synthesis_chain", device,
                         _lib.ptr(a_in), _lib.ptr_array(ds[g0:g1]), _lib.ptr(cur), _lib.ptr(h0),
@@ -194,10 +208,11 @@ class _AnalysisChain(torch.autograd.Function):
     def run(x, h0, h1, mode: int, off: int, n_in: tuple, n_out: tuple):
         """The transform itself (no autograd node)."""
         _lib.require_gpu(x)
-        lead = x.shape[:-1]
-        details, approx = _analysis_chain(_rows(x), h0, h1, mode, off, n_in, n_out)
-        outs = [d.reshape(*lead, d.shape[-1]) for d in details]
-        outs.append(approx.reshape(*lead, approx.shape[-1]))
+        lead = tuple(x.shape[:-1])
+        details, approx = _analysis_chain(_contig(x), h0, h1, mode, off, n_in, n_out, lead)
+        nd = len(lead) + 1
+        outs = [d if d.dim() == nd else d.reshape(*lead, d.shape[-1]) for d in details]
+        outs.append(approx if approx.dim() == nd else approx.reshape(*lead, approx.shape[-1]))
         return tuple(outs)
 
     @staticmethod
@@ -242,10 +257,9 @@ class _SynthesisChain(torch.autograd.Function):
         R = 1
         for s in lead:
             R *= s
-        a2 = _rows(a) if a is not None else None
-        d2 = [(_rows(d) if d is not None else None) for d in ds]
-        y = _synthesis_chain(a2, d2, h0, h1, mode, off, nc, n_out, R, ref.dtype, ref.device)
-        return y.reshape(*lead, n_out[-1])
+        y = _synthesis_chain(_contig(a), [_contig(d) for d in ds], h0, h1, mode, off, nc, n_out,
+                             R, ref.dtype, ref.device, tuple(lead))
+        return y if y.dim() == len(lead) + 1 else y.reshape(*lead, n_out[-1])
 
     @staticmethod
     def backward(ctx, gy):
