@@ -460,7 +460,7 @@ def main():
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-legs", action="store_true",
                     help="skip the configs[0], configs[2] and configs[3] legs")
-    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--cpu-rows", type=int, default=192)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy (HBM counter calibration)")
     a = ap.parse_args()
