@@ -607,7 +607,14 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
   // registers (its first MB_XR NT samples) while the current tile is multiplied, and the last
   // A chunk of a tile is followed by the first chunk of the next tile.  Loads are unconditional
   // from clamped (valid) indices; masks are applied where the values are used.
-  const int pbeg = wave * (TT / 4);
+  // each tile's valid positions, in chunks of 4 MB_U, split evenly over the four waves (a full
+  // tile: a quarter each; a row's last, partial tile: no idle wave)
+  auto wave_range = [&](int nvalid, int& b, int& e) {
+    const int chunk = 4 * MB_U;
+    const int per = ((nvalid + chunk - 1) / chunk + 3) / 4 * chunk;
+    b = min(wave * per, nvalid);
+    e = min(b + per, nvalid);
+  };
   struct Tile {
     const T* grow;  // g of this lane's A row at the tile's first position
     const T* xrow;
@@ -636,6 +643,8 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
   int64_t t = blockIdx.x;
   Tile cur_t = tile_of(t < total ? t : 0);
   load_x(cur_t);
+  int pbeg, pend;
+  wave_range(cur_t.nvalid, pbeg, pend);
   load_a(cur_t, pbeg);
   for (; t < total; t += gridDim.x) {
     const Tile nxt = tile_of(t + gridDim.x < total ? t + gridDim.x : t);
@@ -651,15 +660,16 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
     __syncthreads();
     load_x(nxt);
     const int nvalid = cur_t.nvalid;
-    const int pend = min(pbeg + TT / 4, nvalid);
-    if (pbeg >= pend) load_a(nxt, pbeg);  // no positions of this tile for this wave
+    int nbeg, nend;
+    wave_range(nxt.nvalid, nbeg, nend);
+    if (pbeg >= pend) load_a(nxt, nbeg);  // no positions of this tile for this wave
     for (int c0 = pbeg; c0 < pend; c0 += 4 * MB_U) {
       T cur[MB_U];
 #pragma unroll
       for (int u = 0; u < MB_U; ++u)
         cur[u] = (arow_ok && c0 + 4 * u + kpos < nvalid) ? an[u] : T(0);
       const bool last = c0 + 4 * MB_U >= pend;
-      load_a(last ? nxt : cur_t, last ? pbeg : c0 + 4 * MB_U);
+      load_a(last ? nxt : cur_t, last ? nbeg : c0 + 4 * MB_U);
       // B values: the LDS reads of step u + 1 are issued before the instructions of step u,
       // so an instruction never waits for its own read (fences keep that order; without them
       // the compiler reuses one register and puts a full LDS wait before every instruction)
@@ -685,6 +695,8 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
       }
     }
     cur_t = nxt;
+    pbeg = nbeg;
+    pend = nend;
   }
   // add the four waves' sums (X is free now) and write this workgroup's column
   __syncthreads();
