@@ -1308,7 +1308,7 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
   if (n_out == 0) return FDWT_ERR_ARG;
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
-  {
+  if ((dil & (dil - 1)) == 0) {
     // windowed kernel (power-of-two dilation): tiles over the range g reaches, with the
     // residue-group size D that minimises a cost model of tap work plus staged elements.
     // D >= min(dil, 4): below that the staging gathers runs of 1-2 complex values with
@@ -1333,7 +1333,7 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
                           channels;
       if (!best_d || cost < best_cost) best_d = d, best_cost = cost, best_tiles = tl, best_jb = jb;
     }
-    if ((dil & (dil - 1)) == 0 && best_d) {
+    if (best_d) {
       const int64_t J = TT / best_d;
       const size_t lds =
           (size_t)(best_d * (J + 2 * H) * (RUN + 1) / RUN + best_d) * channels * cs;
