@@ -148,14 +148,17 @@ def attention_flops(m, R, N):
     return 4 * bank + 3 * chain
 
 
-def attention_gpu(steps, warmup, dev):
+ATT_SCALED = (64, 8, 64, 60, 256)  # BASELINE configs[4]'s scaled shape
+
+
+def attention_gpu(steps, warmup, dev, shape=ATT_SHAPE):
     import pytorch_morlet_fdwt_amd as fdwt
-    B, H, C, T, D = ATT_SHAPE
+    B, H, C, T, D = shape
     torch.manual_seed(2)
     m = fdwt.MorletAttention(num_channels=C, hidden_dim=D).to(dev)
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn(*ATT_SHAPE, generator=g).to(dev).requires_grad_()
-    gy = torch.randn(*ATT_SHAPE, generator=torch.Generator().manual_seed(1)).to(dev)
+    x = torch.randn(*shape, generator=torch.Generator(device=dev).manual_seed(0),
+                    device=dev).requires_grad_()
+    gy = torch.randn(*shape, generator=torch.Generator(device=dev).manual_seed(1), device=dev)
     params = [x] + list(m.parameters())
 
     def step():
@@ -178,7 +181,7 @@ def attention_gpu(steps, warmup, dev):
     tokens = B * C * T
     return {"metric": "MorletAttention fwd+bwd tokens/s (B*C*T per step)",
             "value": tokens / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms,
-            "config": {"shape_BHCTD": list(ATT_SHAPE), "freqs": "16 logspace(0, log10(40)) Hz",
+            "config": {"shape_BHCTD": list(shape), "freqs": "16 logspace(0, log10(40)) Hz",
                        "fs": D, "learnable": True, "temperature": 1.0},
             "roofline": {"bound": "valu", "achieved": fl / (ms * 1e-3) / 1e12,
                          "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
@@ -547,6 +550,9 @@ def main():
         line["cwt_cfg3"] = cwt_cfg3(k, a.warmup, dev, cpu)
         line["token_mixer_cfg4"] = token_mixer_cfg4(k, a.warmup, dev, cpu)
         line["dwt_cfg1"] = dwt_cfg1(k, a.warmup, dev, cpu)
+        scaled = attention_gpu(2, 1, dev, ATT_SCALED)
+        scaled["cpu_baseline"] = None  # the CPU oracle needs minutes per step at this size
+        line["morlet_attention_scaled"] = scaled
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(a.cpu_rows)
     print(json.dumps(line))
