@@ -408,7 +408,9 @@ class _MorletMixFunction(torch.autograd.Function):
     Backward: per octave, in row chunks of at most MIX_CHUNK_BYTES of dL/dW, the fused kernel
     writes dL/dW and partial (ga, gb) sums, then the grad-x / grad-h kernels consume it."""
 
-    MIX_CHUNK_BYTES = 256 * 2**20
+    # Row chunks of dL/dW: 2 GiB (the reference uses 256 MiB); on a 288 GB MI355X the larger
+    # chunk costs little memory and cuts the backward's launches 8x at large batch sizes.
+    MIX_CHUNK_BYTES = 2 * 2**30
 
     @staticmethod
     def forward(ctx, x, plan: MorletPlan, H, a, b):
@@ -529,7 +531,8 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
     flash-attention style online softmax (m, l, num) and writes out = num / l in its last
     launch; the backward recomputes the chain and one octave of dL/dW at a time."""
 
-    CHUNK_BYTES = 256 * 2**20
+    # Row chunks of dL/dW: 2 GiB (the reference uses 256 MiB), as MIX_CHUNK_BYTES above.
+    CHUNK_BYTES = 2 * 2**30
 
     @staticmethod
     def forward(ctx, x, plan: MorletPlan, H, V, nch: int, tau: float, precision: str):
