@@ -47,11 +47,43 @@ __device__ inline T load_clamped(const T* __restrict__ p, int64_t i, int64_t n) 
   return (i >= 0 && i < n) ? w : T(0);
 }
 
-// Stage x[row][p0 .. p0 + span) into X (zero outside [0, n)).
+// Stage x[row][p0 .. p0 + span) into X (zero outside [0, n); n >= 1).  Eight loads per thread
+// are issued before any is written to LDS (unconditional, from clamped indices; the range mask
+// is applied at the write): a load-then-write loop waits for each load in turn.
 template <typename T>
 __device__ inline void stage_row(T* X, const T* __restrict__ xrow, int64_t p0, int span,
                                  int64_t n) {
-  for (int k = threadIdx.x; k < span; k += NT) X[k] = load_clamped(xrow, p0 + k, n);
+  constexpr int SB = 8;
+  for (int k0 = 0; k0 < span; k0 += SB * NT) {
+    T v[SB];
+#pragma unroll
+    for (int r = 0; r < SB; ++r)
+      v[r] = xrow[min(max(p0 + k0 + r * NT + threadIdx.x, (int64_t)0), n - 1)];
+#pragma unroll
+    for (int r = 0; r < SB; ++r) {
+      const int k = k0 + r * NT + threadIdx.x;
+      const int64_t i = p0 + k;
+      if (k < span) X[k] = (i >= 0 && i < n) ? v[r] : T(0);
+    }
+  }
+}
+
+// Copy elements [k_begin, k_end) with eight loads per thread in flight: load(k) must be an
+// unconditional load that is valid for every k in the range (clamped indices), store(k, v)
+// applies any mask.  (A load-then-store loop waits for each load in turn.)
+template <typename T, typename LoadF, typename StoreF>
+__device__ inline void batched_copy(int k_begin, int k_end, LoadF&& load, StoreF&& store) {
+  constexpr int SB = 8;
+  for (int k0 = k_begin; k0 < k_end; k0 += SB * NT) {
+    T v[SB];
+#pragma unroll
+    for (int r = 0; r < SB; ++r) v[r] = load(min(k0 + r * NT + (int)threadIdx.x, k_end - 1));
+#pragma unroll
+    for (int r = 0; r < SB; ++r) {
+      const int k = k0 + r * NT + (int)threadIdx.x;
+      if (k < k_end) store(k, v[r]);
+    }
+  }
 }
 
 // Scalogram of positions tid + NT v of the tile for the scale group [s0, s0 + ns), from the
@@ -655,8 +687,13 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
       const int64_t xi = cur_t.xb + i;
       if (i < span) X[skew(i)] = (xi >= 0 && xi < st.n_in) ? xr[r] : T(0);
     }
-    for (int i = tid + MB_XR * NT; i < span; i += NT)
-      X[skew(i)] = load_clamped(cur_t.xrow, cur_t.xb + i, st.n_in);
+    batched_copy<T>(
+        MB_XR * NT, span,
+        [&](int i) { return cur_t.xrow[min(max(cur_t.xb + i, (int64_t)0), st.n_in - 1)]; },
+        [&](int i, T w) {
+          const int64_t xi = cur_t.xb + i;
+          X[skew(i)] = (xi >= 0 && xi < st.n_in) ? w : T(0);
+        });
     __syncthreads();
     load_x(nxt);
     const int nvalid = cur_t.nvalid;
@@ -1271,6 +1308,7 @@ extern "C" int fdwt_morlet_forward(const void* x, const void* taps, void* y, int
   for (int s = 0; s < n_scales; ++s)
     if (chan[s] >= s_total) return FDWT_ERR_ARG;
   if (rows == 0 || n_out == 0) return 0;
+  if (n_in < 1) return FDWT_ERR_ARG;  // x is staged: a row needs a sample
   const int tiles = (int)cdiv(n_out, TT);
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
@@ -1400,6 +1438,7 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   const int64_t K = 2 * (int64_t)half + 1;
   const int64_t n_el = n_scales * K * channels;
   if (rows == 0 || n_out == 0) return 0;
+  if (n_in < 1) return FDWT_ERR_ARG;  // x is staged: a row needs a sample
   const int tiles = (int)cdiv(n_out, TT);
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
@@ -1504,6 +1543,7 @@ extern "C" int fdwt_mix_forward(const void* x, const void* taps, const void* a, 
   for (int s = 0; s < n_scales; ++s)
     if (chan[s] >= s_total) return FDWT_ERR_ARG;
   if (rows == 0 || n_out == 0) return 0;
+  if (n_in < 1) return FDWT_ERR_ARG;  // x is staged: a row needs a sample
   const int tiles = (int)cdiv(n_out, TT);
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
@@ -1542,6 +1582,7 @@ extern "C" int fdwt_mix_backward(const void* x, const void* taps, const void* a,
     if (chan[s] >= s_total) return FDWT_ERR_ARG;
   if (workspace_elems < fdwt_mix_workspace(rows, n_out, n_scales)) return FDWT_ERR_ARG;
   if (rows == 0 || n_out == 0) return 0;
+  if (n_in < 1) return FDWT_ERR_ARG;  // x is staged: a row needs a sample
   const int tiles = (int)cdiv(n_out, TT);
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
@@ -1597,6 +1638,7 @@ extern "C" int fdwt_softmax_forward(const void* x, const void* taps, const void*
   for (int s = 0; s < n_scales; ++s)
     if (chan[s] >= v_s_total) return FDWT_ERR_ARG;
   if (rows == 0 || n_out == 0) return 0;
+  if (n_in < 1) return FDWT_ERR_ARG;  // x is staged: a row needs a sample
   SoftArgs sa{v, v_s_total, nch, v_per_position ? 1 : 0, 0, inv_tau};
   const int tiles = (int)cdiv(n_out, TT);
   hipStream_t hs = static_cast<hipStream_t>(stream);
@@ -1639,6 +1681,7 @@ extern "C" int fdwt_softmax_backward(const void* x, const void* taps, const void
   if (workspace_elems < fdwt_softmax_workspace(rows, n_out, n_scales, v_per_position))
     return FDWT_ERR_ARG;
   if (rows == 0 || n_out == 0) return 0;
+  if (n_in < 1) return FDWT_ERR_ARG;  // x is staged: a row needs a sample
   SoftArgs sa{v, v_s_total, nch, v_per_position ? 1 : 0, row0, inv_tau};
   const int tiles = (int)cdiv(n_out, TT);
   hipStream_t hs = static_cast<hipStream_t>(stream);
