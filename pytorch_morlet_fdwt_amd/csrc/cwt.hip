@@ -47,6 +47,28 @@ __device__ inline T load_clamped(const T* __restrict__ p, int64_t i, int64_t n) 
   return (i >= 0 && i < n) ? w : T(0);
 }
 
+// Raw buffer access to one array of `bytes` < 2^31 bytes: a load takes a 32-bit byte offset
+// (one VGPR instead of a 64-bit address) and returns 0 for any offset outside [0, bytes),
+// negative offsets included (they are range-checked as unsigned).  The resource is built in
+// scalar registers; 0x00020000 is the gfx9 descriptor word 3 (32-bit data format, no swizzle).
+struct BufRsrc {
+  __amdgpu_buffer_rsrc_t r;
+};
+__device__ inline BufRsrc make_rsrc(const void* base, int64_t bytes) {
+  return {__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                            0x00020000)};
+}
+template <typename T>
+__device__ inline T buf_load(BufRsrc b, int byte_off);
+template <>
+__device__ inline float buf_load<float>(BufRsrc b, int byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.r, byte_off, 0, 0));
+}
+template <>
+__device__ inline double buf_load<double>(BufRsrc b, int byte_off) {
+  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(b.r, byte_off, 0, 0));
+}
+
 // Stage x[row][p0 .. p0 + span) into X (zero outside [0, n); n >= 1).  Eight loads per thread
 // are issued before any is written to LDS (unconditional, from clamped indices; the range mask
 // is applied at the write): a load-then-write loop waits for each load in turn.
@@ -313,42 +335,50 @@ __global__ void __launch_bounds__(NT) morlet_adjoint_kernel(Stage st, const T* _
   T acc[RUN];
 #pragma unroll
   for (int k = 0; k < RUN; ++k) acc[k] = T(0);
-  // g position of float element k of the tile (and its channel)
-  auto gpos = [&](int k) -> int64_t {
+  // g is read through a buffer resource per (row, scale) plane: byte offsets are 32-bit (the
+  // host takes this kernel only when every g position a tile touches, -2 dil H .. n_out +
+  // 2 dil H, is within 2^31 bytes of the plane) and positions outside [0, n_out) read as 0.
+  const int qb = (int)qbase;
+  const int dl = (int)dil;
+  auto goff = [&](int k) -> int {
     const int i = k / C;
-    return qbase + (i % D) + dil * (i / D);
+    return ((qb + (i % D) + dl * (i / D)) * C + (k % C)) * (int)sizeof(T);
+  };
+  auto plane = [&](int s) {
+    return make_rsrc(g + ((row * g_scales + st.chan[s]) * st.n_out) * C,
+                     st.n_out * C * (int64_t)sizeof(T));
   };
   constexpr int GPF = sizeof(T) == 8 ? 4 : 8;
   T gr[GPF];
   auto fetch = [&](int s) {
-    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out) * C;
+    const BufRsrc pr = plane(s);
 #pragma unroll
-    for (int e = 0; e < GPF; ++e) {
-      const int k = tid + e * NT;
-      if (e * NT < nel) {
-        const int64_t q = gpos(k);
-        gr[e] = grow[min(max(q, (int64_t)0), st.n_out - 1) * C + (k % C)];
-      }
-    }
+    for (int e = 0; e < GPF; ++e)
+      if (e * NT < nel) gr[e] = buf_load<T>(pr, goff(tid + e * NT));
   };
   const int r = tid % D, b = tid / D;
   const int pb = adj_phys<D>(D * H + r + D * RUN * b);  // phys of U_0
   if (st.n_scales > 0) fetch(0);
   for (int s = 0; s < st.n_scales; ++s) {
-    const T* grow = g + ((row * g_scales + st.chan[s]) * st.n_out) * C;
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < GPF; ++e) {
       const int k = tid + e * NT;
-      if (e * NT < nel && k < nel) {
-        const int64_t q = gpos(k);
-        G[adj_phys<D>(k / C) * C + (k % C)] = (q >= 0 && q < st.n_out) ? gr[e] : T(0);
-      }
+      if (e * NT < nel && k < nel) G[adj_phys<D>(k / C) * C + (k % C)] = gr[e];
     }
-    for (int k = GPF * NT + tid; k < nel; k += NT) {
-      const int64_t q = gpos(k);
-      const T w = grow[min(max(q, (int64_t)0), st.n_out - 1) * C + (k % C)];
-      G[adj_phys<D>(k / C) * C + (k % C)] = (q >= 0 && q < st.n_out) ? w : T(0);
+    {  // the rest of the tile: SB loads per thread in flight before their LDS writes
+      constexpr int SB = 4;
+      const BufRsrc pr = plane(s);
+      for (int k0 = GPF * NT + tid; k0 < nel; k0 += SB * NT) {
+        T v[SB];
+#pragma unroll
+        for (int e = 0; e < SB; ++e) v[e] = buf_load<T>(pr, goff(k0 + e * NT));
+#pragma unroll
+        for (int e = 0; e < SB; ++e) {
+          const int k = k0 + e * NT;
+          if (k < nel) G[adj_phys<D>(k / C) * C + (k % C)] = v[e];
+        }
+      }
     }
     __syncthreads();
     if (s + 1 < st.n_scales) fetch(s + 1);
@@ -1346,9 +1376,12 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
   if (n_out == 0) return FDWT_ERR_ARG;
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
-  if ((dil & (dil - 1)) == 0) {
-    // windowed kernel (power-of-two dilation): tiles over the range g reaches, with the
-    // residue-group size D that minimises a cost model of tap work plus staged elements.
+  if ((dil & (dil - 1)) == 0 &&
+      (n_out + 2 * (int64_t)dil * (half + RUN + 1)) * channels * cs < ((int64_t)1 << 31)) {
+    // windowed kernel (power-of-two dilation, and g positions -2 dil H .. n_out + 2 dil H of
+    // a plane within the 2^31 bytes of its 32-bit buffer offsets): tiles over the range g
+    // reaches, with the residue-group size D that minimises a cost model of tap work plus
+    // staged elements.
     // D >= min(dil, 4): below that the staging gathers runs of 1-2 complex values with
     // stride dil, a cache line per value (on MI355X such tiles ran up to 2x slower than the
     // model predicts; the weight 48 and this floor come from timing every D on the octaves
