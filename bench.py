@@ -151,11 +151,18 @@ def attention_flops(m, R, N):
 ATT_SCALED = (64, 8, 64, 60, 256)  # BASELINE configs[4]'s scaled shape
 
 
-def attention_gpu(steps, warmup, dev, shape=ATT_SHAPE):
+def _att_module(fdwt, channel_mix, C, D):
+    cls = fdwt.MorletChannelMixAttention if channel_mix else fdwt.MorletAttention
+    return cls(num_channels=C, hidden_dim=D)
+
+
+def attention_gpu(steps, warmup, dev, shape=ATT_SHAPE, channel_mix=False):
+    """MorletAttention (or, with ``channel_mix``, MorletChannelMixAttention) forward +
+    backward on x of ``shape``; learnable scales and w0, module-default weights (seed 2)."""
     import pytorch_morlet_fdwt_amd as fdwt
     B, H, C, T, D = shape
     torch.manual_seed(2)
-    m = fdwt.MorletAttention(num_channels=C, hidden_dim=D).to(dev)
+    m = _att_module(fdwt, channel_mix, C, D).to(dev)
     x = torch.randn(*shape, generator=torch.Generator(device=dev).manual_seed(0),
                     device=dev).requires_grad_()
     gy = torch.randn(*shape, generator=torch.Generator(device=dev).manual_seed(1), device=dev)
@@ -178,8 +185,11 @@ def attention_gpu(steps, warmup, dev, shape=ATT_SHAPE):
     ms = e0.elapsed_time(e1) / steps
     R, N = B * H * C, T * D
     fl = attention_flops(m, R, N)
+    if channel_mix:  # U = M x (f x C by C x N per (b, h)): forward, grad-x and grad-M
+        fl += 3 * 2 * m.num_freqs * C * N * B * H
     tokens = B * C * T
-    return {"metric": "MorletAttention fwd+bwd tokens/s (B*C*T per step)",
+    name = "MorletChannelMixAttention" if channel_mix else "MorletAttention"
+    return {"metric": f"{name} fwd+bwd tokens/s (B*C*T per step)",
             "value": tokens / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms,
             "config": {"shape_BHCTD": list(shape), "freqs": "16 logspace(0, log10(40)) Hz",
                        "fs": D, "learnable": True, "temperature": 1.0},
@@ -188,7 +198,7 @@ def attention_gpu(steps, warmup, dev, shape=ATT_SHAPE):
                          "frac": fl / (ms * 1e-3) / FP32_PEAK, "alg_flops": fl}}
 
 
-def attention_cpu(batch=1, reps=3):
+def attention_cpu(batch=1, reps=3, channel_mix=False):
     """The oracle (reference CPU fallback restated, fp32) on a batch-`batch` sample."""
     from oracle import cwt as O
     import pytorch_morlet_fdwt_amd as fdwt
@@ -196,17 +206,18 @@ def attention_cpu(batch=1, reps=3):
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     torch.manual_seed(2)
-    m = fdwt.MorletAttention(num_channels=C, hidden_dim=D)
+    m = _att_module(fdwt, channel_mix, C, D)
     plan = O.Plan(m.cwt.plan.scales, support_margin=1.25)
     x = torch.randn(batch, H, C, T, D, generator=torch.Generator().manual_seed(0))
     ls = m.cwt.log_scales.detach().clone().requires_grad_()
     w0 = torch.tensor(6.0, requires_grad=True)
-    fw = m.freq_weight.detach().clone().requires_grad_()
+    fw = (m.freq_to_channel if channel_mix else m.freq_weight).detach().clone().requires_grad_()
+    op = O.channel_mix_attention if channel_mix else O.attention
 
     def run():
         xx = x.clone().requires_grad_()
         Hf = plan.filters(ls.double().exp(), w0.double(), torch.float32)
-        y = O.attention(xx, plan, Hf, fw, 1.0)
+        y = op(xx, plan, Hf, fw, 1.0)
         torch.autograd.grad(y, [xx, ls, w0, fw], torch.ones_like(y))
 
     run()
@@ -544,6 +555,10 @@ def main():
         if not a.no_cpu_baseline:
             att["cpu_baseline"] = attention_cpu()
         line["morlet_attention"] = att
+        cmix = attention_gpu(max(3, a.steps // 2), a.warmup, dev, channel_mix=True)
+        if not a.no_cpu_baseline:
+            cmix["cpu_baseline"] = attention_cpu(channel_mix=True)
+        line["channel_mix_attention"] = cmix
     if not a.no_legs:
         cpu = not a.no_cpu_baseline
         k = max(3, a.steps // 2)

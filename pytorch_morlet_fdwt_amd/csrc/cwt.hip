@@ -47,6 +47,44 @@ __device__ inline T load_clamped(const T* __restrict__ p, int64_t i, int64_t n) 
   return (i >= 0 && i < n) ? w : T(0);
 }
 
+// Magnitude |W| = sqrt(q) and its reciprocal (0 for q = 0) of a complex value with q = |W|^2,
+// and the exponential of the online softmax.  float32 uses the hardware instructions
+// v_sqrt_f32 / v_rsq_f32 / v_exp_f32 (about 1 ulp each; the correctly rounded library calls
+// cost several times the instructions, comparable to a short filter's taps per scale), with
+// v_rsq_f32's input scaled out of the denormal range; float64 keeps the library functions.
+template <typename T>
+__device__ inline T hw_sqrt(T q) {
+  return sqrt(q);
+}
+template <>
+__device__ inline float hw_sqrt<float>(float q) {
+  return __builtin_amdgcn_sqrtf(q);
+}
+template <typename T>
+__device__ inline void mag_inv(T q, T& mag, T& inv) {
+  mag = sqrt(q);
+  inv = mag > T(0) ? T(1) / mag : T(0);
+}
+template <>
+__device__ inline void mag_inv<float>(float q, float& mag, float& inv) {
+  const bool tiny = q < 0x1p-100f;
+  const float r = __builtin_amdgcn_rsqf(tiny ? q * 0x1p+64f : q);
+  inv = q > 0.0f ? (tiny ? r * 0x1p+32f : r) : 0.0f;
+  mag = q * inv;
+}
+// Online-softmax exponentials: float32 keeps its running maximum in base 2 (v_exp_f32 computes
+// 2^x; |W| / tau is scaled by log2 e once), float64 in base e.  The state in memory is base e.
+template <typename T>
+struct SoftExp {
+  static constexpr T kLog = T(1);
+  static __device__ T ex(T x) { return exp(x); }
+};
+template <>
+struct SoftExp<float> {
+  static constexpr float kLog = 1.44269504088896341f;  // log2 e
+  static __device__ float ex(float x) { return __builtin_amdgcn_exp2f(x); }
+};
+
 // Raw buffer access to one array of `bytes` < 2^31 bytes: a load takes a 32-bit byte offset
 // (one VGPR instead of a 64-bit address) and returns 0 for any offset outside [0, bytes),
 // negative offsets included (they are range-checked as unsigned).  The resource is built in
@@ -868,11 +906,16 @@ __global__ void __launch_bounds__(NT) mix_kernel(Stage st, const T* __restrict__
       for (int v = 0; v < V; ++v) {
         const int64_t n = n0 + tid + NT * v;
         const T rv = re[v][s], iv = im[v][s];
-        const T mag = CPLX ? sqrt(rv * rv + iv * iv) : fabs(rv);
+        T mag = fabs(rv), inv = T(0);
+        if (CPLX) {
+          if (GRAD) mag_inv(fma(rv, rv, iv * iv), mag, inv);
+          else mag = hw_sqrt(fma(rv, rv, iv * iv));
+        } else if (GRAD) {
+          inv = mag > T(0) ? T(1) / mag : T(0);  // rv inv = sign of Re W
+        }
         if (!GRAD) {
           out[v] = fma(av, mag, fma(bv, rv, out[v]));
         } else if (n < st.n_out) {
-          const T inv = mag > T(0) ? T(1) / mag : T(0);
           T* gwp = gw + ((row * st.n_scales + s0 + s) * st.n_out + n) * C;
           if (CPLX) {
             typedef T v2 __attribute__((ext_vector_type(2)));
@@ -960,13 +1003,14 @@ __global__ void __launch_bounds__(NT) softmax_forward_kernel(Stage st, SoftArgs 
             span, st.n_in);
   __syncthreads();
   const T* Vp = static_cast<const T*>(sa.v);
-  const T inv_tau = T(sa.inv_tau);
+  constexpr T kLog = SoftExp<T>::kLog;
+  const T kt = T(sa.inv_tau) * kLog;  // |W| -> |W| / tau in the exponential's base
   T mm[V], ll[V], nn[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int64_t n = n0 + tid + NT * v;
     const int64_t idx = row * st.n_out + min(n, st.n_out - 1);
-    mm[v] = first ? -INFINITY : m[idx];
+    mm[v] = first ? -INFINITY : m[idx] * kLog;
     ll[v] = first ? T(0) : l[idx];
     nn[v] = first ? T(0) : num[idx];
   }
@@ -982,14 +1026,17 @@ __global__ void __launch_bounds__(NT) softmax_forward_kernel(Stage st, SoftArgs 
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const int64_t n = min(n0 + tid + NT * v, st.n_out - 1);
-        const T av = sqrt(re[v][s] * re[v][s] + im[v][s] * im[v][s]) * inv_tau;
+        const T av = hw_sqrt(fma(re[v][s], re[v][s], im[v][s] * im[v][s])) * kt;
         const T val = v_value(sa, Vp, row, gs, n, st.n_out);
-        const T mn = max(mm[v], av);
-        const T alpha = exp(mm[v] - mn);  // exp(-inf) = 0 on the first frequency
-        const T e = exp(av - mn);
-        ll[v] = fma(ll[v], alpha, e);
-        nn[v] = fma(nn[v], alpha, e * val);
-        mm[v] = mn;
+        // one exponential per value: exp(-|av - m|) rescales the state when av is the new
+        // maximum and weighs av otherwise (first frequency: m = -inf, exp(-inf) = 0)
+        const T dd = av - mm[v];
+        const T ex = SoftExp<T>::ex(-fabs(dd));
+        const bool up = dd > T(0);
+        const T sc = up ? ex : T(1), e = up ? T(1) : ex;
+        ll[v] = fma(ll[v], sc, e);
+        nn[v] = fma(nn[v], sc, e * val);
+        mm[v] = up ? av : mm[v];
       }
     }
   }
@@ -998,7 +1045,7 @@ __global__ void __launch_bounds__(NT) softmax_forward_kernel(Stage st, SoftArgs 
     const int64_t n = n0 + tid + NT * v;
     if (n < st.n_out) {
       const int64_t idx = row * st.n_out + n;
-      m[idx] = mm[v];
+      m[idx] = mm[v] * (T(1) / kLog);
       l[idx] = ll[v];
       num[idx] = last ? nn[v] / ll[v] : nn[v];
     }
@@ -1030,13 +1077,15 @@ __global__ void __launch_bounds__(NT) softmax_backward_kernel(Stage st, SoftArgs
   __syncthreads();
   const T* Vp = static_cast<const T*>(sa.v);
   const T inv_tau = T(sa.inv_tau);
+  constexpr T kLog = SoftExp<T>::kLog;
+  const T kt = inv_tau * kLog;
   T mm[V], il[V], oo[V], gg[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int64_t n = n0 + tid + NT * v;
     const int64_t idx = row * st.n_out + min(n, st.n_out - 1);
     const bool ok = n < st.n_out;
-    mm[v] = m[idx];
+    mm[v] = m[idx] * kLog;
     il[v] = T(1) / l[idx];
     oo[v] = out[idx];
     gg[v] = ok ? gy[idx] : T(0);
@@ -1057,11 +1106,11 @@ __global__ void __launch_bounds__(NT) softmax_backward_kernel(Stage st, SoftArgs
         const bool ok = n < st.n_out;
         const int64_t nc = min(n, st.n_out - 1);
         const T rv = re[v][s], iv = im[v][s];
-        const T mag = sqrt(rv * rv + iv * iv);
-        const T p = exp(mag * inv_tau - mm[v]) * il[v];
+        T mag, inv;
+        mag_inv(fma(rv, rv, iv * iv), mag, inv);
+        const T p = SoftExp<T>::ex(fma(mag, kt, -mm[v])) * il[v];
         const T gp = ok ? gg[v] * p : T(0);
         const T val = v_value(sa, Vp, row, gs, nc, st.n_out);
-        const T inv = mag > T(0) ? T(1) / mag : T(0);
         const T coef = gp * (val - oo[v]) * inv_tau * inv;
         if (ok) {
           typedef T v2 __attribute__((ext_vector_type(2)));

@@ -118,3 +118,32 @@ def test_attention_cfg5_full_size():
     ref = OC.attention(x[7:8].double(), plan, H, m.freq_weight.detach().cpu().double(), 1.0)
     got = y[7:8].detach().cpu().double()
     torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
+
+
+def test_channel_mix_attention_cfg5_full_size():
+    """MorletChannelMixAttention num_channels 19, hidden_dim 200 on x
+    (8, 4, 19, 30, 200), forward and backward; batch element 3 against the oracle."""
+    torch.manual_seed(2)
+    m = fdwt.MorletChannelMixAttention(num_channels=19, hidden_dim=200)
+    x = torch.randn(8, 4, 19, 30, 200, generator=torch.Generator().manual_seed(6))
+    gy = torch.randn(8, 4, 19, 30, 200, generator=torch.Generator().manual_seed(7))
+    m = m.to(DEV)
+    xd = x.to(DEV).requires_grad_()
+    y = m(xd)
+    gx, gM = torch.autograd.grad(y, [xd, m.freq_to_channel], gy.to(DEV))
+    plan = OC.Plan(m.cwt.plan.scales, support_margin=1.25)
+    H = plan.filters(m.cwt.log_scales.detach().cpu().double().exp(), 6.0)
+    xr = x[3:4].double().requires_grad_()
+    M = m.freq_to_channel.detach().cpu().double().requires_grad_()
+    ref = OC.channel_mix_attention(xr, plan, H, M, 1.0)
+    rgx, rgM = torch.autograd.grad(ref, [xr, M], gy[3:4].double())
+    torch.testing.assert_close(y[3:4].detach().cpu().double(), ref.detach(), rtol=1e-4,
+                               atol=1e-5 * ref.abs().max().item())
+    torch.testing.assert_close(gx[3:4].cpu().double(), rgx, rtol=1e-4,
+                               atol=1e-5 * rgx.abs().max().item())
+    # dL/dM sums over the whole batch: the oracle's one batch element is a partial sum, so the
+    # full-batch gradient is checked against a float64 GPU run of the same module instead
+    m64 = m.double()
+    y64 = m64(xd.detach().double())
+    gM64, = torch.autograd.grad(y64, [m64.freq_to_channel], gy.to(DEV).double())
+    torch.testing.assert_close(gM.double(), gM64, rtol=1e-4, atol=1e-5 * gM64.abs().max().item())
