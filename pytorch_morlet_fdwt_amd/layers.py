@@ -83,6 +83,43 @@ class WaveletTokenMixer(nn.Module):
         return y.transpose(1, 2)
 
 
+class _ChannelProject(torch.autograd.Function):
+    """U = M v for M (f, C) and v (G, C, N) -> (G, f, N) (layers.py:257-259 of the reference,
+    an einsum there).  The backward's dL/dM = sum_(g, n) gU v^T is a product with a long
+    inner dimension (G N) and a tiny result (f x C): a batched product over G alone gives one
+    output tile per batch looping over all N, which leaves most of the GPU idle.  Here the
+    inner dimension is split into chunks of ``KCHUNK`` samples, one batch each, and the
+    partial products are summed in a fixed order."""
+
+    KCHUNK = 512
+
+    @staticmethod
+    def forward(ctx, M, v):
+        ctx.save_for_backward(M, v)
+        return torch.matmul(M, v)
+
+    @staticmethod
+    def backward(ctx, gU):
+        M, v = ctx.saved_tensors
+        gM = gv = None
+        if ctx.needs_input_grad[1]:
+            gv = torch.matmul(M.t().contiguous(), gU)
+        if ctx.needs_input_grad[0]:
+            G, C, N = v.shape
+            f = M.shape[0]
+            kc = _ChannelProject.KCHUNK
+            nk = -(-N // kc)
+
+            def chunks(t, rows):  # (G, rows, N) -> (G nk, rows, kc), zero-padded
+                tp = t.new_zeros((G, rows, nk * kc))
+                tp[..., :N] = t
+                return tp.view(G, rows, nk, kc).transpose(1, 2).reshape(G * nk, rows, kc)
+
+            vt = chunks(v, C).transpose(1, 2).contiguous()  # (G nk, kc, C)
+            gM = torch.bmm(chunks(gU.contiguous(), f), vt).sum(0)
+        return gM, gv
+
+
 class _MorletPatchAttention(nn.Module):
     """(B, H, C, T, D) patch tokens flattened to (B, H, C, T*D) signals sampled at
     ``hidden_dim / patch_duration`` Hz, and a learnable Morlet CWT (layers.py:112-162)."""
@@ -183,5 +220,5 @@ class MorletChannelMixAttention(_MorletPatchAttention):
         B, H, C, T, D = self._check(x)
         dt = torch.float64 if x.dtype == torch.float64 else torch.float32
         v = x.reshape(B, H, C, T * D).to(dt)
-        U = torch.matmul(self.freq_to_channel.to(dt), v)  # (B, H, f, T*D)
+        U = _ChannelProject.apply(self.freq_to_channel.to(dt), v.reshape(B * H, C, T * D))
         return self._spectral_softmax(x, U.reshape(B * H, self.num_freqs, T * D))
