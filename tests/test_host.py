@@ -43,6 +43,29 @@ def test_argument_errors_are_rejected_before_launch():
     assert lib.fdwt_chain_max_length(16, 0) > 16384
 
 
+def test_bank_entry_points_reject_empty_input_rows():
+    """A bank stage stages x into LDS, so rows of zero samples with outputs to produce are an
+    argument error (returned before any launch; the pointers are never dereferenced)."""
+    import ctypes
+    lib = _lib.lib()
+    dummy = ctypes.c_void_p(256)
+    sup = (ctypes.c_int32 * 1)(2)
+    chan = (ctypes.c_int32 * 1)(0)
+    # x, taps, y, rows, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels,
+    # s_total, dtype, stream
+    assert lib.fdwt_morlet_forward(dummy, dummy, dummy, 1, 0, 5, 0, 1, 2, sup, chan, 1, 2, 1,
+                                   0, None) == -1
+    # no rows, or no outputs: nothing to do
+    assert lib.fdwt_morlet_forward(dummy, dummy, dummy, 0, 0, 5, 0, 1, 2, sup, chan, 1, 2, 1,
+                                   0, None) == 0
+    assert lib.fdwt_morlet_forward(dummy, dummy, dummy, 1, 0, 0, 0, 1, 2, sup, chan, 1, 2, 1,
+                                   0, None) == 0
+    # x, taps, v, v_per_position, v_s_total, nch, m, l, num, rows, n_in, n_out, x_off,
+    # n_scales, half, support, chan, dil, inv_tau, first, last, dtype, stream
+    assert lib.fdwt_softmax_forward(dummy, dummy, dummy, 0, 1, 1, dummy, dummy, dummy, 1, 0, 5,
+                                    0, 1, 2, sup, chan, 1, 1.0, 1, 1, 0, None) == -1
+
+
 def test_cpu_tensors_fail_loudly():
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         fdwt.dwt(torch.randn(2, 64), "db4")
