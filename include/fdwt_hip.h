@@ -108,7 +108,9 @@ int64_t fdwt_chain_max_length(int32_t taps, int32_t dtype);
  * (and im when channels == 2); real parts must be even and imaginary parts odd around c, as
  * every Morlet filter is.  support[s] (non-decreasing) bounds the non-zero taps of scale s,
  * chan[s] is its output channel.  support / chan are host arrays of n_scales entries
- * (n_scales <= FDWT_CWT_MAX_SCALES).  Compute dtypes: FDWT_F32 or FDWT_F64.
+ * (n_scales <= FDWT_CWT_MAX_SCALES).  Compute dtypes: FDWT_F32 or FDWT_F64.  Calls with
+ * rows == 0 or n_out == 0 do nothing; otherwise the stage entry points that read x
+ * (forward, backward_h, mix, softmax) need n_in >= 1 and return FDWT_ERR_ARG for n_in == 0.
  */
 #define FDWT_CWT_MAX_SCALES 64
 
