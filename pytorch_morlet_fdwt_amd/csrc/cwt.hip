@@ -167,7 +167,15 @@ __device__ inline void bank_group(const T* __restrict__ X, const T* __restrict__
       im[v][s] = T(0);
     }
   }
+  // per-scale rows of the tap table (scalar registers, fixed over the tap loop) and one 32-bit
+  // byte offset shared by all of them: a scalar load per scale and tap with the offset in a
+  // register, instead of a 64-bit address rebuilt per scale and tap
+  const char* trow[SG];
+#pragma unroll
+  for (int s = 0; s < SG; ++s)
+    trow[s] = reinterpret_cast<const char*>(taps + (int64_t)(s0 + min(s, ns - 1)) * (half + 1) * C);
   for (int t = 1; t <= tmax; ++t) {
+    const unsigned toff = (unsigned)(t * C * (int)sizeof(T));
     T ps[V], ms[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -179,7 +187,7 @@ __device__ inline void bank_group(const T* __restrict__ X, const T* __restrict__
 #pragma unroll
     for (int s = 0; s < SG; ++s) {
       if (s < ns) {
-        const T* tp = taps + ((s0 + s) * (half + 1) + t) * C;
+        const T* tp = reinterpret_cast<const T*>(trow[s] + toff);
         const T hr = tp[0];
 #pragma unroll
         for (int v = 0; v < V; ++v) re[v][s] = fma(hr, ps[v], re[v][s]);
