@@ -102,6 +102,19 @@ def step_bytes(R):
     return total, per_kernel
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (first processor in /proc/cpuinfo), for the baseline record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(rows=16, reps=3):
     """The oracle (reference CPU fallback restated, fp32) on `rows` rows of every combo."""
     from oracle import dwt as O
@@ -131,6 +144,7 @@ def cpu_baseline(rows=16, reps=3):
     t = statistics.median(ts)
     total, _ = step_bytes(rows)
     return {"value": total / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"the full 20-combination step on {rows} of {SHAPE[0] * SHAPE[1]} rows, "
                       f"fp32, torch {torch.__version__} CPU, median of {reps} after 1 warm-up "
                       f"({t:.2f} s per step)"}
@@ -228,6 +242,7 @@ def attention_cpu(batch=1, reps=3, channel_mix=False):
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
     return {"value": batch * C * T / t, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"B={batch} of {B} (shape {[batch, H, C, T, D]}), fp32, learnable scales "
                       f"and w0, median of {reps} after 1 warm-up ({t:.2f} s per step)"}
 
@@ -318,7 +333,7 @@ def dwt_cfg1(steps, warmup, dev, cpu):
         t, threads = _cpu_median(run)
         out["cpu_baseline"] = {
             "value": 4 * rows * (2 * DWT1_N + 2 * m + 4 * C) / t / 1e9, "unit": "GB/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{rows} of {R} rows, fp32, median of 3 after 1 warm-up ({t:.3f} s)"}
     return out
 
@@ -386,7 +401,7 @@ def cwt_cfg3(steps, warmup, dev, cpu):
 
         t, threads = _cpu_median(run)
         out["cpu_baseline"] = {"value": rows * CWT3_N / t, "unit": "samples/s",
-                               "cores": threads, "kind": "port",
+                               "cores": threads, "kind": "port", "cpu_model": cpu_model(),
                                "sample": f"{rows} of {R} rows, fp32, median of 3 after 1 "
                                          f"warm-up ({t:.3f} s)"}
     return out
@@ -447,7 +462,7 @@ def token_mixer_cfg4(steps, warmup, dev, cpu):
 
         t, threads = _cpu_median(run)
         out["cpu_baseline"] = {"value": N * rows / D / t, "unit": "tokens/s",
-                               "cores": threads, "kind": "port",
+                               "cores": threads, "kind": "port", "cpu_model": cpu_model(),
                                "sample": f"batch 1 of {B}, {rows} of {D} feature rows (tokens "
                                          f"counted pro rata), no out_proj, fp32, median of 3 "
                                          f"after 1 warm-up ({t:.3f} s)"}

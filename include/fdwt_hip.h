@@ -193,12 +193,6 @@ int fdwt_mix_backward(const void* x, const void* taps, const void* a, const void
                       const int32_t* chan, int32_t dil, int32_t channels, int32_t s_total,
                       int32_t d_dim, int64_t row0, int32_t dtype, void* stream);
 
-/* out[o] (+)= sum over the rows * per_row items of partial[item * n_el + o], in a fixed
- * order (deterministic counterpart of the reference's atomic accumulations). */
-int fdwt_reduce_rows(const void* partial, void* out, int64_t rows, int64_t per_row,
-                     int64_t n_el, int64_t stride_row, int32_t accumulate, int32_t dtype,
-                     void* stream);
-
 /* Spectral softmax stage, replacing `forward_stage` / `backward_stage`
  * (src/fdwt/kernels/softmax.py:195-210).  a_f = |W_f| * inv_tau; V is per channel
  * ((nch, v_s_total), row r uses V[(r + row0) % nch]) or per position ((G, v_s_total, n_out),

@@ -165,3 +165,21 @@ def waverec(coeffs, w="db4", mode="symmetric"):
         a = idwt(a, d, w, mode)
     return a
 
+
+
+def wavelet_token_mixer(x, w, mode, level, bands):
+    """layers.py:75-109 (WaveletTokenMixer.forward): x (B, L, D) -> wavedec along L of every
+    channel, band j of [cA_J, cD_J .. cD_1] mapped across channels by bands[j] -- (W, b) for
+    one Linear, (W1, b1, W2, b2) for Linear -> GELU -> Linear -- then waverec, cropped to L."""
+    L = x.shape[1]
+    coeffs = wavedec(x.transpose(1, 2), w, mode, level)  # (B, D, n_j)
+    mixed = []
+    for c, p in zip(coeffs, bands):
+        t = c.transpose(1, 2)
+        if len(p) == 2:
+            t = torch.nn.functional.linear(t, p[0], p[1])
+        else:
+            t = torch.nn.functional.linear(
+                torch.nn.functional.gelu(torch.nn.functional.linear(t, p[0], p[1])), p[2], p[3])
+        mixed.append(t.transpose(1, 2))
+    return waverec(mixed, w, mode)[..., :L].transpose(1, 2)

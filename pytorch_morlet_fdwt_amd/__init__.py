@@ -1,15 +1,21 @@
-"""MI355X-native wavelet transforms for PyTorch-ROCm (drop-in for pytorch_morlet_fdwt).
+"""``pytorch_morlet_fdwt_amd`` -- the fdwt filter-bank transforms as hand-written HIP
+kernels for MI355X (gfx950), behind the same Python names as ``pytorch_morlet_fdwt``.
 
-* :func:`dwt`, :func:`idwt`, :func:`wavedec`, :func:`waverec`, :class:`DWT1D`,
-  :class:`IDWT1D` -- Mallat fast wavelet transform (O(N)), PyWavelets-compatible.
-* :func:`cwt`, :class:`CWT1D` -- Morlet continuous wavelet transform with an O(N)-per-scale
-  octave pyramid (``method="fast"``).
-* :class:`MorletTokenMixer`, :class:`WaveletTokenMixer`, :class:`MorletAttention`,
-  :class:`MorletChannelMixAttention` -- attention replacements.
+What it provides:
 
-Every operator runs hand-written HIP kernels for gfx950 (``libfdwt_hip.so``, C ABI in
-``include/fdwt_hip.h``) on ROCm tensors; there is no CPU fallback.  Use
-``import pytorch_morlet_fdwt_amd as fdwt`` in code written for the reference.
+* discrete wavelet transforms with PyWavelets semantics -- single level (``dwt`` /
+  ``idwt``), multilevel (``wavedec`` / ``waverec``, every level fused into one kernel
+  launch per direction) and their modules ``DWT1D`` / ``IDWT1D``;
+* the Morlet continuous wavelet transform (``cwt``, ``CWT1D``; plans through
+  ``MorletPlan``, frequency/scale conversion helpers), computed octave by octave;
+* sequence layers built on both: ``MorletTokenMixer`` and ``WaveletTokenMixer`` for
+  (batch, length, dim) tokens, ``MorletAttention`` and ``MorletChannelMixAttention`` for
+  (B, H, C, T, D) patch tokens, where the scalogram is reduced on chip and never stored.
+
+Tensors must live on a ROCm device: the kernels in ``libfdwt_hip.so`` (C ABI in
+``include/fdwt_hip.h``) are the only implementation, and a missing library or a CPU tensor
+raises instead of falling back.  Existing code switches with
+``import pytorch_morlet_fdwt_amd as fdwt``.
 """
 
 from . import config

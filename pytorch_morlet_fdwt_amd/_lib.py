@@ -53,7 +53,6 @@ SIGNATURES = {
                          _I32, _I32, _I32, _I32, _I64, _I32, _I32, _P],
     "fdwt_mix_backward": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
                           _PI32, _PI32, _I32, _I32, _I32, _I32, _I64, _I32, _P],
-    "fdwt_reduce_rows": [_P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _P],
     "fdwt_softmax_forward": [_P, _P, _P, _I32, _I64, _I32, _P, _P, _P, _I64, _I64, _I64, _I64,
                              _I32, _I32, _PI32, _PI32, _I32, _DBL, _I32, _I32, _I32, _P],
     "fdwt_softmax_workspace": [_I64, _I64, _I32, _I32],

@@ -1144,18 +1144,6 @@ __global__ void __launch_bounds__(NT) softmax_backward_kernel(Stage st, SoftArgs
 }
 
 // ------------------------------------------------------------------ deterministic reductions
-// out[o] (+)= sum_{i < count} in[i * stride_i + o * stride_o] (fixed order), o < n_out_el
-template <typename T>
-__global__ void reduce_strided_kernel(const T* __restrict__ in, T* __restrict__ out, int64_t n,
-                                      int64_t count, int64_t stride_i, int64_t stride_o,
-                                      int accumulate) {
-  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= n) return;
-  T acc = T(0);
-  for (int64_t i = 0; i < count; ++i) acc += in[i * stride_i + o * stride_o];
-  out[o] = accumulate ? out[o] + acc : acc;
-}
-
 // out[o] (+)= sum_{i < count} in[o * count + i]: one workgroup per output, fixed order
 // (per-thread strided sums, then a fixed shuffle / LDS tree).
 template <typename T>
@@ -1694,23 +1682,6 @@ extern "C" int fdwt_mix_backward(const void* x, const void* taps, const void* a,
   if (channels == 2) MIXB(double, true);
   MIXB(double, false);
 #undef MIXB
-}
-
-extern "C" int fdwt_reduce_rows(const void* partial, void* out, int64_t rows, int64_t per_row,
-                                int64_t n_el, int64_t stride_row, int32_t accumulate,
-                                int32_t dtype, void* stream) {
-  // out[o] (+)= sum_{r < rows} sum_{j < per_row} partial[r * stride_row + j * n_el + o]
-  if (!partial || !out || rows < 0 || per_row < 0 || n_el < 0 ||
-      (dtype != FDWT_F32 && dtype != FDWT_F64))
-    return FDWT_ERR_ARG;
-  if (n_el == 0) return 0;
-  if (stride_row != per_row * n_el) return FDWT_ERR_ARG;  // contiguous (rows x per_row) items
-  hipStream_t hs = static_cast<hipStream_t>(stream);
-  if (dtype == FDWT_F32)
-    return launch(reduce_strided_kernel<float>, cdiv(n_el, NT), 0, hs, (const float*)partial,
-                  (float*)out, n_el, rows * per_row, n_el, (int64_t)1, (int)accumulate);
-  return launch(reduce_strided_kernel<double>, cdiv(n_el, NT), 0, hs, (const double*)partial,
-                (double*)out, n_el, rows * per_row, n_el, (int64_t)1, (int)accumulate);
 }
 
 extern "C" int fdwt_softmax_forward(const void* x, const void* taps, const void* v,

@@ -16,6 +16,7 @@
 //    prefetched into registers while the current chunk is computed.
 //  * Split kernels (one level, several workgroups per row) serve rows too long for LDS.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -1478,19 +1479,21 @@ int launch_schain(const SChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
   return 0;
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device, cached per device.  The cache entries are atomics:
+// concurrent first calls from several host threads may each query the device, and they all
+// store the same value.
 inline int device_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cache[dev]) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 // Workgroups of a persistent whole-row kernel: as many as fit on the device at once (by its

@@ -132,10 +132,15 @@ class MorletPlan:
         return [i * self.channels + c for i in st.scale_idx for c in range(self.channels)]
 
     def filter_geometry(self):
-        """Per-scale dilation and half support as ctypes int32 arrays (filter kernels)."""
+        """Per-scale dilation and half support as ctypes int32 arrays (filter kernels), one
+        pair per chunk of at most FDWT_MORLET_MAX_FILTERS scales: [(i0, i1, dil, sup)]."""
         if "geom" not in self._cache:
-            self._cache["geom"] = (_i32([int(d) for d in self._dil]),
-                                   _i32([int(c) for c in self._sup]))
+            S = self.num_scales
+            self._cache["geom"] = [
+                (i0, min(S, i0 + _MAX_FILTERS),
+                 _i32([int(d) for d in self._dil[i0:i0 + _MAX_FILTERS]]),
+                 _i32([int(c) for c in self._sup[i0:i0 + _MAX_FILTERS]]))
+                for i0 in range(0, S, _MAX_FILTERS)]
         return self._cache["geom"]
 
     def w0_device(self, w0, device: torch.device) -> torch.Tensor:
@@ -175,9 +180,6 @@ class MorletPlan:
         one HIP kernel builds the bank and one computes its gradient; on the CPU (host-side
         planning and inspection) it is the torch expression below."""
         if scales.is_cuda:
-            if self.num_scales > _MAX_FILTERS:
-                raise ValueError(f"at most {_MAX_FILTERS} scales per Morlet bank on the device, "
-                                 f"got {self.num_scales}")
             return _MorletFiltersFunction.apply(scales, w0, self, dtype)
         dev = scales.device
         f64 = torch.float64
@@ -212,10 +214,11 @@ class _MorletFiltersFunction(torch.autograd.Function):
         w = plan.w0_device(w0, dev)
         H = torch.empty((plan.num_scales * plan.channels, 2 * plan.center + 1), device=dev,
                         dtype=_out_dtype(dtype))
-        dil, sup = plan.filter_geometry()
-        _lib.launch("fdwt_morlet_filters", dev, _lib.ptr(s), _lib.ptr(w), dil, sup,
-                    plan.num_scales, plan.center, plan.channels, int(plan.norm == "l2"),
-                    _lib.ptr(H), _lib.dtype_code(H.dtype), _lib.stream(dev))
+        for i0, i1, dil, sup in plan.filter_geometry():
+            _lib.launch("fdwt_morlet_filters", dev, _lib.ptr(s[i0:]), _lib.ptr(w), dil, sup,
+                        i1 - i0, plan.center, plan.channels, int(plan.norm == "l2"),
+                        _lib.ptr(H[i0 * plan.channels:]), _lib.dtype_code(H.dtype),
+                        _lib.stream(dev))
         ctx.plan, ctx.w0_tensor = plan, isinstance(w0, torch.Tensor)
         ctx.scales_dtype = scales.dtype
         ctx.w0_meta = (w0.dtype, w0.shape) if ctx.w0_tensor else None
@@ -230,16 +233,19 @@ class _MorletFiltersFunction(torch.autograd.Function):
         gH = gH.contiguous()
         if gH.dtype not in (torch.float32, torch.float64):
             gH = gH.float()
-        g = torch.empty(plan.num_scales + 1, device=dev, dtype=torch.float64)
-        dil, sup = plan.filter_geometry()
-        _lib.launch("fdwt_morlet_filters_backward", dev, _lib.ptr(s), _lib.ptr(w), dil, sup,
-                    plan.num_scales, plan.center, plan.channels, int(plan.norm == "l2"),
-                    _lib.ptr(gH), _lib.dtype_code(gH.dtype), _lib.ptr(g),
-                    _lib.ptr(g[plan.num_scales:]), _lib.stream(dev))
+        geom = plan.filter_geometry()
+        S = plan.num_scales
+        # g[:S] = d/ds per scale; g[S + c] = chunk c's share of d/dw0, summed in chunk order
+        g = torch.empty(S + len(geom), device=dev, dtype=torch.float64)
+        for c, (i0, i1, dil, sup) in enumerate(geom):
+            _lib.launch("fdwt_morlet_filters_backward", dev, _lib.ptr(s[i0:]), _lib.ptr(w), dil,
+                        sup, i1 - i0, plan.center, plan.channels, int(plan.norm == "l2"),
+                        _lib.ptr(gH[i0 * plan.channels:]), _lib.dtype_code(gH.dtype),
+                        _lib.ptr(g[i0:]), _lib.ptr(g[S + c:]), _lib.stream(dev))
         g_s = g[:plan.num_scales].to(ctx.scales_dtype)
         g_w0 = None
         if ctx.w0_tensor:
-            g_w0 = g[plan.num_scales].to(ctx.w0_meta[0]).reshape(ctx.w0_meta[1])
+            g_w0 = (g[S] if len(geom) == 1 else g[S:].sum()).to(ctx.w0_meta[0]).reshape(ctx.w0_meta[1])
         return g_s, g_w0, None, None
 
 
@@ -253,12 +259,33 @@ def _i32(values):
     return (ctypes.c_int32 * max(1, len(values)))(*[int(v) for v in values])
 
 
-def _stage_args(plan: MorletPlan, k: int):
-    st = plan.stages[k]
-    if len(st.scale_idx) > _MAX_STAGE_SCALES:
-        raise ValueError(f"an octave holds {len(st.scale_idx)} scales; at most "
-                         f"{_MAX_STAGE_SCALES} are supported per octave")
-    return st, _i32(st.support), _i32(st.scale_idx), _i32(range(len(st.scale_idx)))
+@dataclass
+class _Group:
+    """One launch of a stage: its scales g0 .. g1 - 1 (in the stage's support order; each
+    stage kernel takes at most FDWT_CWT_MAX_SCALES of them, so an octave with more scales is
+    launched in consecutive groups with the octave's dilation and tap table)."""
+    g0: int
+    g1: int
+    sup: object    # ctypes int32 supports of the group (non-decreasing)
+    chan: object   # ctypes int32 global scale indices (output channels of the scalogram)
+    local: object  # ctypes int32 0 .. g1 - g0 - 1 (channels of a per-group dL/dW)
+
+    @property
+    def n(self) -> int:
+        return self.g1 - self.g0
+
+
+def _stage_groups(plan: MorletPlan, k: int) -> List[_Group]:
+    key = ("groups", k)
+    if key not in plan._cache:
+        st = plan.stages[k]
+        n = len(st.scale_idx)
+        plan._cache[key] = [
+            _Group(g0, min(n, g0 + _MAX_STAGE_SCALES), _i32(st.support[g0:g0 + _MAX_STAGE_SCALES]),
+                   _i32(st.scale_idx[g0:g0 + _MAX_STAGE_SCALES]),
+                   _i32(range(min(n, g0 + _MAX_STAGE_SCALES) - g0)))
+            for g0 in range(0, n, _MAX_STAGE_SCALES)]
+    return plan._cache[key]
 
 
 def _lowpass_step(plan: MorletPlan, xj: torch.Tensor, j: int, N: int) -> torch.Tensor:
@@ -296,24 +323,28 @@ def _lowpass_chain(plan: MorletPlan, x: torch.Tensor) -> List[torch.Tensor]:
     return xs
 
 
-def _stage_backward(plan, k, xj, g, g_scales, chan, taps, gx, accumulate, need_h):
-    """grad-x (accumulated into gx) and, if asked, the tap gradient (S_j, 2 half + 1, C)."""
-    st, sup, _, _ = _stage_args(plan, k)
+def _stage_backward(plan, k, grp: _Group, xj, g, g_scales, chan, taps, gx, accumulate,
+                    need_h):
+    """grad-x of one launch group (accumulated into gx) and, if asked, the group's tap
+    gradient (g1 - g0, 2 half + 1, C).  ``chan`` gives the group's channels in g, ``taps``
+    is the stage's whole tap table."""
+    st = plan.stages[k]
     R, n_out = g.shape[0], g.shape[2]
     C = plan.channels
     mj = plan.margins[st.octave]
     dev, dt = g.device, g.dtype
-    _lib.launch("fdwt_morlet_backward_x", dev, _lib.ptr(g), _lib.ptr(taps), _lib.ptr(gx), R,
-                gx.shape[1], n_out, mj, len(st.scale_idx), st.half, sup, chan, st.dil, C,
+    tg = taps[grp.g0:grp.g1]
+    _lib.launch("fdwt_morlet_backward_x", dev, _lib.ptr(g), _lib.ptr(tg), _lib.ptr(gx), R,
+                gx.shape[1], n_out, mj, grp.n, st.half, grp.sup, chan, st.dil, C,
                 g_scales, int(accumulate), _lib.dtype_code(dt), _lib.stream(dev))
     if not need_h:
         return None
     L = _lib.lib()
-    ws_n = L.fdwt_morlet_backward_h_workspace(R, n_out, len(st.scale_idx), st.half, C)
+    ws_n = L.fdwt_morlet_backward_h_workspace(R, n_out, grp.n, st.half, C)
     ws = torch.empty(max(1, ws_n), device=dev, dtype=dt)
-    gh = torch.empty((len(st.scale_idx), 2 * st.half + 1, C), device=dev, dtype=dt)
+    gh = torch.empty((grp.n, 2 * st.half + 1, C), device=dev, dtype=dt)
     _lib.launch("fdwt_morlet_backward_h", dev, _lib.ptr(xj), _lib.ptr(g), _lib.ptr(ws), ws_n,
-                _lib.ptr(gh), R, xj.shape[1], n_out, mj, len(st.scale_idx), st.half, sup, chan,
+                _lib.ptr(gh), R, xj.shape[1], n_out, mj, grp.n, st.half, grp.sup, chan,
                 st.dil, C, g_scales, 0, _lib.dtype_code(dt), _lib.stream(dev))
     return gh
 
@@ -346,12 +377,13 @@ class _MorletCWTFunction(torch.autograd.Function):
         for j in range(plan.n_octaves):
             if j in by_oct:
                 k = by_oct[j]
-                st, sup, chan, _ = _stage_args(plan, k)
+                st = plan.stages[k]
                 taps = tables[k] = plan.stage_taps(H, k)
-                _lib.launch("fdwt_morlet_forward", x.device, _lib.ptr(xs[j]), _lib.ptr(taps),
-                            _lib.ptr(y), R, xs[j].shape[1], N, plan.margins[j],
-                            len(st.scale_idx), st.half, sup, chan, st.dil, C, plan.num_scales,
-                            _lib.dtype_code(x.dtype), _lib.stream(x.device))
+                for grp in _stage_groups(plan, k):
+                    _lib.launch("fdwt_morlet_forward", x.device, _lib.ptr(xs[j]),
+                                _lib.ptr(taps[grp.g0:grp.g1]), _lib.ptr(y), R, xs[j].shape[1], N,
+                                plan.margins[j], grp.n, st.half, grp.sup, grp.chan, st.dil, C,
+                                plan.num_scales, _lib.dtype_code(x.dtype), _lib.stream(x.device))
             if j + 1 < plan.n_octaves:
                 xs.append(_lowpass_step(plan, xs[j], j, N))
         ctx.plan = plan
@@ -382,13 +414,16 @@ class _MorletCWTFunction(torch.autograd.Function):
                 filled = False
             if j in by_oct:
                 k = by_oct[j]
-                st, sup, chan, _ = _stage_args(plan, k)
                 taps = ctx.tables[k]  # the forward's compact tap tables
-                gh = _stage_backward(plan, k, xs[j] if ctx.need_h else None, g, plan.num_scales,
-                                     chan, taps, gx, filled, ctx.need_h)
-                filled = True
-                if gh is not None:
-                    _scatter_gh(plan, gH, k, gh)
+                ghs = []
+                for grp in _stage_groups(plan, k):
+                    gh = _stage_backward(plan, k, grp, xs[j] if ctx.need_h else None, g,
+                                         plan.num_scales, grp.chan, taps, gx, filled, ctx.need_h)
+                    filled = True
+                    if gh is not None:
+                        ghs.append(gh)
+                if ghs:
+                    _scatter_gh(plan, gH, k, ghs[0] if len(ghs) == 1 else torch.cat(ghs))
             if not filled:
                 gx.zero_()
             g_next = gx
@@ -428,14 +463,16 @@ class _MorletMixFunction(torch.autograd.Function):
         for j in range(plan.n_octaves):
             if j in by_oct:
                 k = by_oct[j]
-                st, sup, chan, _ = _stage_args(plan, k)
+                st = plan.stages[k]
                 taps = tables[k] = plan.stage_taps(H, k)
-                _lib.launch("fdwt_mix_forward", x.device, _lib.ptr(xs[j]), _lib.ptr(taps),
-                            _lib.ptr(a_), _lib.ptr(b_), _lib.ptr(y), R, xs[j].shape[1], N,
-                            plan.margins[j], len(st.scale_idx), st.half, sup, chan, st.dil,
-                            plan.channels, a_.shape[1], D, 0, 0 if first else 1,
-                            _lib.dtype_code(dt), _lib.stream(x.device))
-                first = False
+                for grp in _stage_groups(plan, k):
+                    _lib.launch("fdwt_mix_forward", x.device, _lib.ptr(xs[j]),
+                                _lib.ptr(taps[grp.g0:grp.g1]), _lib.ptr(a_), _lib.ptr(b_),
+                                _lib.ptr(y), R, xs[j].shape[1], N, plan.margins[j], grp.n,
+                                st.half, grp.sup, grp.chan, st.dil, plan.channels, a_.shape[1],
+                                D, 0, 0 if first else 1, _lib.dtype_code(dt),
+                                _lib.stream(x.device))
+                    first = False
             if j + 1 < plan.n_octaves:
                 xs.append(_lowpass_step(plan, xs[j], j, N))
         if first:
@@ -476,35 +513,40 @@ class _MorletMixFunction(torch.autograd.Function):
                 filled = False
             if j in by_oct:
                 k = by_oct[j]
-                st, sup, chan, local = _stage_args(plan, k)
-                S_j = len(st.scale_idx)
+                st = plan.stages[k]
                 taps = ctx.tables[k]  # the forward's compact tap tables
-                chunk = max(1, _MorletMixFunction.MIX_CHUNK_BYTES // (S_j * N * C * gy.element_size()))
-                gh_acc = None
-                for r0, r1 in _stage_chunks(R, chunk, D):
-                    rc = r1 - r0
-                    gw = torch.empty((rc, S_j, N, C), device=dev, dtype=dt)
-                    ws_n = L.fdwt_mix_workspace(rc, N, S_j)
-                    ws = torch.empty(max(1, ws_n), device=dev, dtype=dt)
-                    xj = xs[j][r0:r1]
-                    _lib.launch("fdwt_mix_backward", dev, _lib.ptr(xj), _lib.ptr(taps),
-                                _lib.ptr(a), _lib.ptr(b), _lib.ptr(gy[r0:r1]), _lib.ptr(gw),
-                                _lib.ptr(ws), ws_n, rc, xj.shape[1], N, mj, S_j, st.half, sup,
-                                chan, st.dil, C, a.shape[1], D, r0, _lib.dtype_code(dt),
-                                _lib.stream(dev))
-                    # (rows, tiles, S_j, 2) -> per weight row d (rows are whole multiples of D)
-                    part = ws[:ws_n].view(rc, -1, S_j, 2).sum(1).view(-1, D, S_j, 2).sum(0)
-                    idx = plan._index(k, dev)
-                    ga[:, idx] += part[..., 0]
-                    gb[:, idx] += part[..., 1]
-                    gh = _stage_backward(plan, k, xj, gw, S_j, local, taps, gx[r0:r1],
-                                         filled, need_h)
-                    if gh is not None:
-                        gh_acc = gh if gh_acc is None else gh_acc + gh
-                    del gw
-                if gh_acc is not None:
-                    _scatter_gh(plan, gH, k, gh_acc)
-                filled = True
+                idx = plan._index(k, dev)
+                ghs = []
+                for grp in _stage_groups(plan, k):
+                    S_g = grp.n
+                    chunk = max(1, _MorletMixFunction.MIX_CHUNK_BYTES // (S_g * N * C * gy.element_size()))
+                    gh_acc = None
+                    tg = taps[grp.g0:grp.g1]
+                    for r0, r1 in _stage_chunks(R, chunk, D):
+                        rc = r1 - r0
+                        gw = torch.empty((rc, S_g, N, C), device=dev, dtype=dt)
+                        ws_n = L.fdwt_mix_workspace(rc, N, S_g)
+                        ws = torch.empty(max(1, ws_n), device=dev, dtype=dt)
+                        xj = xs[j][r0:r1]
+                        _lib.launch("fdwt_mix_backward", dev, _lib.ptr(xj), _lib.ptr(tg),
+                                    _lib.ptr(a), _lib.ptr(b), _lib.ptr(gy[r0:r1]), _lib.ptr(gw),
+                                    _lib.ptr(ws), ws_n, rc, xj.shape[1], N, mj, S_g, st.half,
+                                    grp.sup, grp.chan, st.dil, C, a.shape[1], D, r0,
+                                    _lib.dtype_code(dt), _lib.stream(dev))
+                        # (rows, tiles, S_g, 2) -> per weight row d (rows are whole multiples of D)
+                        part = ws[:ws_n].view(rc, -1, S_g, 2).sum(1).view(-1, D, S_g, 2).sum(0)
+                        ga[:, idx[grp.g0:grp.g1]] += part[..., 0]
+                        gb[:, idx[grp.g0:grp.g1]] += part[..., 1]
+                        gh = _stage_backward(plan, k, grp, xj, gw, S_g, grp.local, taps,
+                                             gx[r0:r1], filled, need_h)
+                        if gh is not None:
+                            gh_acc = gh if gh_acc is None else gh_acc + gh
+                        del gw
+                    filled = True
+                    if gh_acc is not None:
+                        ghs.append(gh_acc)
+                if ghs:
+                    _scatter_gh(plan, gH, k, ghs[0] if len(ghs) == 1 else torch.cat(ghs))
             if not filled:
                 gx.zero_()
             g_next = gx
@@ -551,17 +593,22 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
         last_j = max(by_oct)
         tables = {}
         xj = x
+        first = True
         for j in range(plan.n_octaves):
             if j in by_oct:
                 k = by_oct[j]
-                st, sup, chan, _ = _stage_args(plan, k)
+                st = plan.stages[k]
                 taps = tables[k] = plan.stage_taps(H, k)
-                _lib.launch("fdwt_softmax_forward", x.device, _lib.ptr(xj), _lib.ptr(taps),
-                            _lib.ptr(V_), int(v_pos), V_.shape[1], nch, _lib.ptr(m), _lib.ptr(l),
-                            _lib.ptr(out), R, xj.shape[1], N, plan.margins[j],
-                            len(st.scale_idx), st.half, sup, chan, st.dil, 1.0 / tau,
-                            int(k == 0), int(j == last_j), _lib.dtype_code(dt),
-                            _lib.stream(x.device))
+                groups = _stage_groups(plan, k)
+                for gi, grp in enumerate(groups):
+                    last = j == last_j and gi + 1 == len(groups)
+                    _lib.launch("fdwt_softmax_forward", x.device, _lib.ptr(xj),
+                                _lib.ptr(taps[grp.g0:grp.g1]), _lib.ptr(V_), int(v_pos),
+                                V_.shape[1], nch, _lib.ptr(m), _lib.ptr(l), _lib.ptr(out), R,
+                                xj.shape[1], N, plan.margins[j], grp.n, st.half, grp.sup,
+                                grp.chan, st.dil, 1.0 / tau, int(first), int(last),
+                                _lib.dtype_code(dt), _lib.stream(x.device))
+                    first = False
             if j + 1 < plan.n_octaves and j < last_j:
                 xj = _lowpass_step(plan, xj, j, N)
         ctx.plan, ctx.nch, ctx.tau = plan, nch, tau
@@ -596,39 +643,45 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
                 filled = False
             if j in by_oct:
                 k = by_oct[j]
-                st, sup, chan, local = _stage_args(plan, k)
-                S_j = len(st.scale_idx)
+                st = plan.stages[k]
                 taps = ctx.tables[k]  # the forward's compact tap tables
                 idx = plan._index(k, dev)
-                chunk = max(1, _SpectralSoftmaxFunction.CHUNK_BYTES // (S_j * N * 2 * gy.element_size()))
-                gh_acc = None
-                for r0, r1 in _stage_chunks(R, chunk, nch):
-                    rc = r1 - r0
-                    gw = torch.empty((rc, S_j, N, 2), device=dev, dtype=dt)
-                    ws_n = L.fdwt_softmax_workspace(rc, N, S_j, int(v_pos))
-                    ws = torch.empty(max(1, ws_n), device=dev, dtype=dt)
-                    xj = xs[j][r0:r1]
-                    _lib.launch("fdwt_softmax_backward", dev, _lib.ptr(xj), _lib.ptr(taps),
-                                _lib.ptr(V), int(v_pos), V.shape[1], nch, r0, _lib.ptr(m[r0:r1]),
-                                _lib.ptr(l[r0:r1]), _lib.ptr(out[r0:r1]), _lib.ptr(gy[r0:r1]),
-                                _lib.ptr(gw), _lib.ptr(ws), ws_n, rc, xj.shape[1], N, mj, S_j,
-                                st.half, sup, chan, st.dil, 1.0 / ctx.tau, _lib.dtype_code(dt),
-                                _lib.stream(dev))
-                    if v_pos:
-                        # (rows, S_j, N): sum the nch rows of each group
-                        part = ws[:ws_n].view(rc // nch, nch, S_j, N).sum(1)
-                        gV[r0 // nch:r1 // nch, idx] += part
-                    else:
-                        part = ws[:ws_n].view(rc, -1, S_j).sum(1).view(-1, nch, S_j).sum(0)
-                        gV[:, idx] += part
-                    gh = _stage_backward(plan, k, xj, gw, S_j, local, taps, gx[r0:r1],
-                                         filled, need_h)
-                    if gh is not None:
-                        gh_acc = gh if gh_acc is None else gh_acc + gh
-                    del gw
-                if gh_acc is not None:
-                    _scatter_gh(plan, gH, k, gh_acc)
-                filled = True
+                ghs = []
+                for grp in _stage_groups(plan, k):
+                    S_g = grp.n
+                    gidx = idx[grp.g0:grp.g1]
+                    tg = taps[grp.g0:grp.g1]
+                    chunk = max(1, _SpectralSoftmaxFunction.CHUNK_BYTES // (S_g * N * 2 * gy.element_size()))
+                    gh_acc = None
+                    for r0, r1 in _stage_chunks(R, chunk, nch):
+                        rc = r1 - r0
+                        gw = torch.empty((rc, S_g, N, 2), device=dev, dtype=dt)
+                        ws_n = L.fdwt_softmax_workspace(rc, N, S_g, int(v_pos))
+                        ws = torch.empty(max(1, ws_n), device=dev, dtype=dt)
+                        xj = xs[j][r0:r1]
+                        _lib.launch("fdwt_softmax_backward", dev, _lib.ptr(xj), _lib.ptr(tg),
+                                    _lib.ptr(V), int(v_pos), V.shape[1], nch, r0,
+                                    _lib.ptr(m[r0:r1]), _lib.ptr(l[r0:r1]), _lib.ptr(out[r0:r1]),
+                                    _lib.ptr(gy[r0:r1]), _lib.ptr(gw), _lib.ptr(ws), ws_n, rc,
+                                    xj.shape[1], N, mj, S_g, st.half, grp.sup, grp.chan, st.dil,
+                                    1.0 / ctx.tau, _lib.dtype_code(dt), _lib.stream(dev))
+                        if v_pos:
+                            # (rows, S_g, N): sum the nch rows of each group
+                            part = ws[:ws_n].view(rc // nch, nch, S_g, N).sum(1)
+                            gV[r0 // nch:r1 // nch, gidx] += part
+                        else:
+                            part = ws[:ws_n].view(rc, -1, S_g).sum(1).view(-1, nch, S_g).sum(0)
+                            gV[:, gidx] += part
+                        gh = _stage_backward(plan, k, grp, xj, gw, S_g, grp.local, taps,
+                                             gx[r0:r1], filled, need_h)
+                        if gh is not None:
+                            gh_acc = gh if gh_acc is None else gh_acc + gh
+                        del gw
+                    filled = True
+                    if gh_acc is not None:
+                        ghs.append(gh_acc)
+                if ghs:
+                    _scatter_gh(plan, gH, k, ghs[0] if len(ghs) == 1 else torch.cat(ghs))
             if not filled:
                 gx.zero_()
             g_next = gx

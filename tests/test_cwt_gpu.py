@@ -372,3 +372,87 @@ def test_device_filters_gradcheck():
     H = p.filters(ls.exp(), 6.0, f64)
     (g,) = torch.autograd.grad(H.square().sum(), ls)
     assert torch.isfinite(g).all() and g.abs().max() > 0
+
+
+MANY = {
+    # method "direct" puts every scale in one octave: 150 scales, launched as 64 + 64 + 22
+    "direct_150": dict(scales=list(np.geomspace(1.0, 40.0, 150)), method="direct", n=400),
+    # a linear grid: octave 5 of the fast plan holds 128 scales (and octave 4 64 + more)
+    "fast_255": dict(scales=list(np.arange(1.0, 256.0)), method="fast", n=700),
+    # more filters than one filter-kernel launch builds (256): two filter chunks
+    "direct_300": dict(scales=list(np.geomspace(1.0, 12.0, 300)), method="direct", n=150),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MANY))
+def test_many_scales_per_octave_match_oracle(name):
+    """Octaves with more scales than one stage launch takes (FDWT_CWT_MAX_SCALES = 64) and
+    banks with more filters than one filter launch builds (256) run as consecutive launch
+    groups: values and every gradient against the oracle in float64."""
+    kw = MANY[name]
+    m = fdwt.CWT1D(scales=kw["scales"], method=kw["method"], learnable=True,
+                   learnable_w0=True).to(DEV).double()
+    assert max(len(st.scale_idx) for st in m.plan.stages) > 64
+    g = torch.Generator().manual_seed(len(kw["scales"]))
+    x = torch.randn(3, kw["n"], dtype=f64, generator=g)
+    gy = torch.randn(3, len(kw["scales"]), kw["n"], 2, dtype=f64, generator=g)
+    xx = x.to(DEV).requires_grad_()
+    y = m(xx)
+    (torch.view_as_real(y) * gy.to(DEV)).sum().backward()
+    plan = O.Plan(m.plan.scales, method=kw["method"], support_margin=1.25)
+    ls = m.log_scales.detach().cpu().clone().requires_grad_()
+    w0 = torch.tensor(6.0, dtype=f64, requires_grad=True)
+    xr = x.clone().requires_grad_()
+    ref = O.apply_plan(xr, plan, plan.filters(ls.exp(), w0))
+    (torch.view_as_real(ref) * gy).sum().backward()
+    for nm, got, want in (("y", y.detach(), ref.detach()), ("gx", xx.grad, xr.grad),
+                          ("g_log_scales", m.log_scales.grad, ls.grad), ("g_w0", m.w0.grad, w0.grad)):
+        got = got.cpu()
+        if got.is_complex():
+            got, want = torch.view_as_real(got), torch.view_as_real(want)
+        torch.testing.assert_close(got.double(), want.double(), rtol=0,
+                                   atol=1e-10 * max(want.abs().max().item(), 1e-300),
+                                   msg=lambda s: f"{nm}: {s}")
+
+
+def test_many_scales_mix_and_softmax_match_oracle():
+    """The fused mix and spectral softmax over a 130-scale direct plan (three launch groups
+    per octave) against the oracle, with gradients."""
+    scales = list(np.geomspace(1.0, 30.0, 130))
+    m = fdwt.CWT1D(scales=scales, method="direct", learnable=True, learnable_w0=True)
+    m = m.to(DEV).double()
+    g = torch.Generator().manual_seed(130)
+    B, D, N = 2, 3, 300
+    x = torch.randn(B, D, N, dtype=f64, generator=g)
+    a = torch.randn(D, 130, dtype=f64, generator=g)
+    b = torch.randn(D, 130, dtype=f64, generator=g)
+    V = torch.randn(B, 130, N, dtype=f64, generator=g)
+    plan = O.Plan(m.plan.scales, method="direct", support_margin=1.25)
+    for kind in ("mix", "softmax"):
+        m.zero_grad()
+        xx, aa, bb, VV = (t.to(DEV).requires_grad_() for t in (x, a, b, V))
+        H = m.plan.filters(m.log_scales.exp(), m.w0, f64)
+        if kind == "mix":
+            y = CWTM.morlet_mix(xx, m.plan, H, aa, bb)
+        else:
+            y = CWTM.spectral_softmax(xx.reshape(B * D, N), m.plan, H, VV, D, 0.7)
+        (y.square()).sum().backward()
+        ls = m.log_scales.detach().cpu().clone().requires_grad_()
+        w0 = torch.tensor(6.0, dtype=f64, requires_grad=True)
+        xr, ar, br, Vr = (t.clone().requires_grad_() for t in (x, a, b, V))
+        Hr = plan.filters(ls.exp(), w0)
+        if kind == "mix":
+            ref = O.morlet_mix(xr, plan, Hr, ar, br)
+        else:
+            ref = O.spectral_softmax(xr.reshape(B * D, N), plan, Hr, Vr, D, 0.7)
+        ref.square().sum().backward()
+        pairs = [("y", y.detach(), ref.detach()), ("gx", xx.grad, xr.grad),
+                 ("g_log_scales", m.log_scales.grad, ls.grad), ("g_w0", m.w0.grad, w0.grad)]
+        if kind == "mix":
+            pairs += [("ga", aa.grad, ar.grad), ("gb", bb.grad, br.grad)]
+        else:
+            pairs += [("gV", VV.grad, Vr.grad)]
+        for nm, got, want in pairs:
+            torch.testing.assert_close(got.cpu().double(), want.double(), rtol=0,
+                                       atol=1e-10 * max(want.abs().max().item(), 1e-300),
+                                       msg=lambda s: f"{kind} {nm}: {s}")

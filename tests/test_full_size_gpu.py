@@ -63,6 +63,38 @@ def test_dwt_sweep_full_size(wavelet, mode, n):
     assert abs(lhs - rhs) <= ADJ_TOL * scale
 
 
+def test_dwt_cfg0_full_batch():
+    """db4, symmetric, level 5 on x (32, 64, 2500) fp32, the benchmark's launch:
+    rows spread over the batch against the oracle, perfect reconstruction and the adjoint
+    identity over the whole batch."""
+    n = 2500
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(32, 64, n, generator=g)
+    xd = x.to(DEV).requires_grad_()
+    coeffs = fdwt.wavedec(xd, "db4", "symmetric", 5)
+    assert [c.shape[-1] for c in coeffs] == [84, 84, 162, 318, 630, 1253]
+    ref = OD.wavedec(x.reshape(-1, n)[ROWS].double(), "db4", "symmetric", 5)
+    for c, r in zip(coeffs, ref):
+        torch.testing.assert_close(c.detach().reshape(-1, c.shape[-1])[ROWS].cpu().double(), r,
+                                   atol=1e-6, rtol=1e-5)
+    rec = fdwt.waverec(coeffs, "db4", "symmetric")
+    assert rec.shape == (32, 64, n)
+    refr = OD.waverec([r for r in ref], "db4", "symmetric")
+    torch.testing.assert_close(rec.detach().reshape(-1, n)[ROWS].cpu().double(), refr,
+                               atol=1e-6, rtol=1e-5)
+    scale = max(1.0, x.abs().max().item())
+    torch.testing.assert_close(rec.detach().cpu(), x, atol=1e-6 * scale, rtol=1e-5)
+    # adjoint identity of the benchmark's whole step: forward (analysis then synthesis chain)
+    # against its backward (analysis chain of the upstream gradient, then synthesis chain)
+    gy = torch.randn(rec.shape, generator=g).to(DEV)
+    gx, = torch.autograd.grad(rec, xd, gy)
+    lhs = _inner(rec.detach(), gy)
+    rhs = _inner(xd.detach(), gx)
+    assert abs(lhs - rhs) <= ADJ_TOL * _norm(rec.detach()) * _norm(gy)
+    # the round trip is the identity on an orthogonal bank, so is its transpose
+    torch.testing.assert_close(gx, gy, atol=1e-6 * max(1.0, gy.abs().max().item()), rtol=1e-5)
+
+
 def test_cwt_cfg3_full_size():
     """fast CWT, 40 freqs logspace(-0.3, 2) Hz at fs 250 on x (32, 64, 2500)."""
     freqs = np.logspace(-0.3, 2, 40)
@@ -88,36 +120,99 @@ def test_cwt_cfg3_full_size():
     assert abs(lhs - rhs) <= ADJ_TOL * _norm(yr) * _norm(gr)
 
 
-def test_token_mixer_cfg4_full_size():
-    """configs[3]: MorletTokenMixer dim 256, 16 freqs logspace(0, 1.8) Hz, fs 250, Xavier
-    mixing weights, x (8, 4096, 256); batch element 5 against the oracle."""
+def _token_mixer_cfg4():
     torch.manual_seed(2)
     m = fdwt.MorletTokenMixer(256, freqs=torch.logspace(0, 1.8, 16).tolist(), fs=250.0)
     torch.nn.init.xavier_uniform_(m.mag_weight)
     torch.nn.init.xavier_uniform_(m.phase_weight)
-    x = torch.randn(8, 4096, 256, generator=torch.Generator().manual_seed(4))
-    y = m.to(DEV)(x.to(DEV))
+    return m
+
+
+def _oracle_token_mixer(m, x):
     plan = OC.Plan(m.cwt.plan.scales, support_margin=1.25)
-    H = plan.filters(m.cwt.log_scales.detach().cpu().double().exp(), 6.0)
-    p = {k: v.detach().cpu().double() for k, v in m.named_parameters()}
-    ref = OC.token_mixer(x[5:6].double(), plan, H, p["mag_weight"], p["phase_weight"], p["bias"],
-                         p["out_proj.weight"], p["out_proj.bias"])
-    got = y[5:6].detach().cpu().double()
-    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
+    p = {k: v.detach().cpu().double().requires_grad_() for k, v in m.named_parameters()}
+    H = plan.filters(p["cwt.log_scales"].exp(), 6.0)
+    y = OC.token_mixer(x, plan, H, p["mag_weight"], p["phase_weight"], p["bias"],
+                       p["out_proj.weight"], p["out_proj.bias"])
+    return y, p
+
+
+def test_token_mixer_cfg4_full_size():
+    """configs[3]: MorletTokenMixer dim 256, 16 freqs logspace(0, 1.8) Hz, fs 250, Xavier
+    mixing weights, x (8, 4096, 256), forward and backward.  Batch element 5 of the full-batch
+    run against the oracle (output and input gradient: rows of different batch elements never
+    meet); parameter gradients of the full batch against a float64 GPU run, and of a one-element
+    GPU run against the oracle."""
+    m = _token_mixer_cfg4().to(DEV)
+    x = torch.randn(8, 4096, 256, generator=torch.Generator().manual_seed(4))
+    gy = torch.randn(8, 4096, 256, generator=torch.Generator().manual_seed(8))
+    xd = x.to(DEV).requires_grad_()
+    y = m(xd)
+    params = [p for p in m.parameters() if p.requires_grad]
+    grads = torch.autograd.grad(y, [xd] + params, gy.to(DEV))
+    xr = x[5:6].double().requires_grad_()
+    ref, p_ref = _oracle_token_mixer(m, xr)
+    rgx, = torch.autograd.grad(ref, [xr], gy[5:6].double())
+    torch.testing.assert_close(y[5:6].detach().cpu().double(), ref.detach(), rtol=1e-4,
+                               atol=1e-5 * ref.abs().max().item())
+    torch.testing.assert_close(grads[0][5:6].cpu().double(), rgx, rtol=1e-4,
+                               atol=1e-5 * rgx.abs().max().item())
+    # full-batch parameter gradients against float64 on the GPU
+    m64 = _token_mixer_cfg4().to(DEV).double()
+    m64.load_state_dict(m.state_dict())
+    y64 = m64(xd.detach().double())
+    p64 = [p for p in m64.parameters() if p.requires_grad]
+    g64 = torch.autograd.grad(y64, p64, gy.to(DEV).double())
+    names = [n for n, p in m.named_parameters() if p.requires_grad]
+    for nm, a, b in zip(names, grads[1:], g64):
+        torch.testing.assert_close(a.double(), b, rtol=1e-4, atol=3e-5 * b.abs().max().item(),
+                                   msg=lambda s: f"{nm}: {s}")
+    # one batch element on the GPU: parameter gradients against the oracle
+    m.zero_grad()
+    y1 = m(x[5:6].to(DEV))
+    g1 = torch.autograd.grad(y1, params, gy[5:6].to(DEV))
+    rp = torch.autograd.grad(ref, [p_ref[n] for n in names], gy[5:6].double())
+    for nm, a, b in zip(names, g1, rp):
+        torch.testing.assert_close(a.cpu().double(), b, rtol=1e-4, atol=3e-5 * b.abs().max().item(),
+                                   msg=lambda s: f"{nm}: {s}")
 
 
 def test_attention_cfg5_full_size():
-    """configs[4]: MorletAttention num_channels 19, hidden_dim 200 on x (8, 4, 19, 30, 200);
-    batch element 7 against the oracle."""
+    """MorletAttention num_channels 19, hidden_dim 200 on x (8, 4, 19, 30, 200),
+    forward and backward: batch element 7 against the oracle (output, input gradient), the
+    full batch's parameter gradients against a float64 GPU run, a one-element GPU run's
+    parameter gradients against the oracle."""
     torch.manual_seed(2)
-    m = fdwt.MorletAttention(num_channels=19, hidden_dim=200)
+    m = fdwt.MorletAttention(num_channels=19, hidden_dim=200).to(DEV)
     x = torch.randn(8, 4, 19, 30, 200, generator=torch.Generator().manual_seed(5))
-    y = m.to(DEV)(x.to(DEV))
+    gy = torch.randn(8, 4, 19, 30, 200, generator=torch.Generator().manual_seed(9))
+    xd = x.to(DEV).requires_grad_()
+    y = m(xd)
+    names = [n for n, _ in m.named_parameters()]
+    params = list(m.parameters())
+    grads = torch.autograd.grad(y, [xd] + params, gy.to(DEV))
     plan = OC.Plan(m.cwt.plan.scales, support_margin=1.25)
-    H = plan.filters(m.cwt.log_scales.detach().cpu().double().exp(), 6.0)
-    ref = OC.attention(x[7:8].double(), plan, H, m.freq_weight.detach().cpu().double(), 1.0)
-    got = y[7:8].detach().cpu().double()
-    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item())
+    p_ref = {n: p.detach().cpu().double().requires_grad_() for n, p in m.named_parameters()}
+    H = plan.filters(p_ref["cwt.log_scales"].exp(), p_ref["cwt.w0"])
+    xr = x[7:8].double().requires_grad_()
+    ref = OC.attention(xr, plan, H, p_ref["freq_weight"], 1.0)
+    rg = torch.autograd.grad(ref, [xr] + [p_ref[n] for n in names], gy[7:8].double())
+    torch.testing.assert_close(y[7:8].detach().cpu().double(), ref.detach(), rtol=1e-4,
+                               atol=1e-5 * ref.abs().max().item())
+    torch.testing.assert_close(grads[0][7:8].cpu().double(), rg[0], rtol=1e-4,
+                               atol=1e-5 * rg[0].abs().max().item())
+    m64 = fdwt.MorletAttention(num_channels=19, hidden_dim=200).to(DEV).double()
+    m64.load_state_dict(m.state_dict())
+    y64 = m64(xd.detach().double())
+    g64 = torch.autograd.grad(y64, list(m64.parameters()), gy.to(DEV).double())
+    for nm, a, b in zip(names, grads[1:], g64):
+        torch.testing.assert_close(a.double(), b, rtol=1e-4, atol=3e-5 * b.abs().max().item(),
+                                   msg=lambda s: f"{nm}: {s}")
+    y1 = m(x[7:8].to(DEV))
+    g1 = torch.autograd.grad(y1, params, gy[7:8].to(DEV))
+    for nm, a, b in zip(names, g1, rg[1:]):
+        torch.testing.assert_close(a.cpu().double(), b, rtol=1e-4, atol=3e-5 * b.abs().max().item(),
+                                   msg=lambda s: f"{nm}: {s}")
 
 
 def test_channel_mix_attention_cfg5_full_size():
@@ -147,3 +242,39 @@ def test_channel_mix_attention_cfg5_full_size():
     y64 = m64(xd.detach().double())
     gM64, = torch.autograd.grad(y64, [m64.freq_to_channel], gy.to(DEV).double())
     torch.testing.assert_close(gM.double(), gM64, rtol=1e-4, atol=1e-5 * gM64.abs().max().item())
+
+
+SCALED = (64, 8, 64, 60, 256)
+
+
+@pytest.mark.parametrize("cls", ["MorletAttention", "MorletChannelMixAttention"])
+def test_attention_scaled_cfg5_group(cls):
+    """The scaled configs[4] shape (64, 8, 64, 60, 256): its own plan (fs 256), the largest
+    R x N of the benchmark (32768 x 15360) and dL/dW chunks near the 2 GiB default.  The full
+    batch runs forward and backward on the GPU; one whole (b, h) group of 64 channels (the
+    channel mix couples a group's channels, never two groups) is checked against the oracle:
+    output and input gradient."""
+    torch.set_num_threads(max(1, min(16, len(__import__("os").sched_getaffinity(0)))))
+    torch.manual_seed(2)
+    m = getattr(fdwt, cls)(num_channels=64, hidden_dim=256).to(DEV)
+    B, Hh, C, T, D = SCALED
+    gen = torch.Generator(device=DEV).manual_seed(12)
+    xd = torch.randn(SCALED, device=DEV, generator=gen).requires_grad_()
+    gy = torch.randn(SCALED, device=DEV, generator=gen)
+    y = m(xd)
+    gx, = torch.autograd.grad(y, [xd], gy)
+    assert torch.isfinite(gx).all()
+    b, h = 41, 5
+    plan = OC.Plan(m.cwt.plan.scales, support_margin=1.25)
+    H = plan.filters(m.cwt.log_scales.detach().cpu().double().exp(), m.cwt.w0.detach().cpu().double())
+    xr = xd.detach()[b:b + 1, h:h + 1].cpu().double().requires_grad_()
+    W = (m.freq_weight if cls == "MorletAttention" else m.freq_to_channel).detach().cpu().double()
+    if cls == "MorletAttention":
+        ref = OC.attention(xr, plan, H, W, 1.0)
+    else:
+        ref = OC.channel_mix_attention(xr, plan, H, W, 1.0)
+    rgx, = torch.autograd.grad(ref, [xr], gy[b:b + 1, h:h + 1].cpu().double())
+    torch.testing.assert_close(y[b:b + 1, h:h + 1].detach().cpu().double(), ref.detach(), rtol=1e-4,
+                               atol=1e-5 * ref.abs().max().item())
+    torch.testing.assert_close(gx[b:b + 1, h:h + 1].cpu().double(), rgx, rtol=1e-4,
+                               atol=1e-5 * rgx.abs().max().item())

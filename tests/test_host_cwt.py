@@ -110,3 +110,24 @@ def test_module_parameters_match_reference_names():
         assert stored, name
     stored = {k[len("tm/tm_f3/param/"):] for k in G.files if k.startswith("tm/tm_f3/param/")}
     assert stored == set(t.state_dict())
+
+
+def test_resolve_precision_rule():
+    """src/fdwt/kernels/conv.py:332-338: fp64 is always exact, bf16 / fp16 inputs or
+    allow_bf16 give bf16 operands, allow_tf32 alone gives tf32."""
+    from pytorch_morlet_fdwt_amd import config
+    saved = config.allow_tf32, config.allow_bf16
+    try:
+        config.allow_tf32, config.allow_bf16 = False, False
+        assert config.resolve_precision(torch.float32) == "ieee"
+        assert config.resolve_precision(torch.float64) == "ieee"
+        assert config.resolve_precision(torch.bfloat16) == "bf16"
+        assert config.resolve_precision(torch.float16) == "bf16"
+        assert config.resolve_precision(torch.float16, torch.float64) == "ieee"
+        config.allow_tf32 = True
+        assert config.resolve_precision(torch.float32) == "tf32"
+        config.allow_bf16 = True
+        assert config.resolve_precision(torch.float32) == "bf16"
+        assert config.resolve_precision(torch.float64) == "ieee"
+    finally:
+        config.allow_tf32, config.allow_bf16 = saved
