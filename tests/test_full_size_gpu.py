@@ -152,7 +152,9 @@ def test_token_mixer_cfg4_full_size():
     grads = torch.autograd.grad(y, [xd] + params, gy.to(DEV))
     xr = x[5:6].double().requires_grad_()
     ref, p_ref = _oracle_token_mixer(m, xr)
-    rgx, = torch.autograd.grad(ref, [xr], gy[5:6].double())
+    names = [n for n, p in m.named_parameters() if p.requires_grad]
+    rg = torch.autograd.grad(ref, [xr] + [p_ref[n] for n in names], gy[5:6].double())
+    rgx, rp = rg[0], rg[1:]
     torch.testing.assert_close(y[5:6].detach().cpu().double(), ref.detach(), rtol=1e-4,
                                atol=1e-5 * ref.abs().max().item())
     torch.testing.assert_close(grads[0][5:6].cpu().double(), rgx, rtol=1e-4,
@@ -163,7 +165,6 @@ def test_token_mixer_cfg4_full_size():
     y64 = m64(xd.detach().double())
     p64 = [p for p in m64.parameters() if p.requires_grad]
     g64 = torch.autograd.grad(y64, p64, gy.to(DEV).double())
-    names = [n for n, p in m.named_parameters() if p.requires_grad]
     for nm, a, b in zip(names, grads[1:], g64):
         torch.testing.assert_close(a.double(), b, rtol=1e-4, atol=3e-5 * b.abs().max().item(),
                                    msg=lambda s: f"{nm}: {s}")
@@ -171,7 +172,6 @@ def test_token_mixer_cfg4_full_size():
     m.zero_grad()
     y1 = m(x[5:6].to(DEV))
     g1 = torch.autograd.grad(y1, params, gy[5:6].to(DEV))
-    rp = torch.autograd.grad(ref, [p_ref[n] for n in names], gy[5:6].double())
     for nm, a, b in zip(names, g1, rp):
         torch.testing.assert_close(a.cpu().double(), b, rtol=1e-4, atol=3e-5 * b.abs().max().item(),
                                    msg=lambda s: f"{nm}: {s}")
