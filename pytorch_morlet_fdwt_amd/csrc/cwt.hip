@@ -1194,8 +1194,8 @@ struct FilterArgs {
 #define FDWT_FILTER_ARGS(name)                                              \
   typedef __attribute__((address_space(4))) const FilterArgs FArgs_;         \
   FArgs_& name = *(FArgs_*)__builtin_amdgcn_kernarg_segment_ptr()
-#else
-#define FDWT_FILTER_ARGS(name) const FilterArgs& name = *static_cast<const FilterArgs*>(nullptr)
+#else  // the host pass only type-checks kernel bodies
+#define FDWT_FILTER_ARGS(name) const FilterArgs name {}
 #endif
 
 struct MorletSample {

@@ -217,7 +217,7 @@ struct SynArgs {
 // returns false when a set overflows (then nothing is prefetched).
 template <typename F>
 inline bool syn_regs(int J, const int32_t* nc, const void* approx, const void* const* details,
-                     int ZL, int yP, int yQ, int yD, F&& emit) {
+                     int ZL, int yP, int yQ, int yD, int nt, F&& emit) {
   int ka = 0, kb = 0;
   for (int s = 0; s <= J; ++s) {
     const int l = s == 0 ? 0 : s - 1;
@@ -226,10 +226,10 @@ inline bool syn_regs(int J, const int32_t* nc, const void* approx, const void* c
     if (!ptr || cnt <= 0) continue;
     const bool tail = l == J - 1;
     const int dest = (s == 0 ? syn_src(0, J, yP, yQ) : syn_dbuf(l, J, yQ, yD)) + ZL;
-    for (int c0 = 0; c0 < cnt; c0 += NT) {
+    for (int c0 = 0; c0 < cnt; c0 += nt) {
       int& k = tail ? kb : ka;
       if (k == (tail ? PB : PA)) return false;
-      emit(tail, k, c0, cnt - c0 < NT ? cnt - c0 : NT, dest + c0, l, s == 0);
+      emit(tail, k, c0, cnt - c0 < nt ? cnt - c0 : nt, dest + c0, l, s == 0);
       ++k;
     }
   }
@@ -469,7 +469,7 @@ __device__ inline void fill_margins(T* buf, int n, int pmin, int pmax, int mode)
   const int P = mode_period(mode, n);
   const int left = -pmin;                      // positions pmin .. -1
   const int right = pmax >= n ? pmax - n + 1 : 0;
-  for (int k = threadIdx.x; k < left + right; k += NT) {
+  for (int k = threadIdx.x; k < left + right; k += blockDim.x) {
     const int p = k < left ? pmin + k : n + (k - left);
     bool valid;
     const int i = ext_index(p, n, mode, P, valid);
@@ -480,7 +480,7 @@ __device__ inline void fill_margins(T* buf, int n, int pmin, int pmax, int mode)
 template <typename T>
 __device__ inline void load_taps(const T* __restrict__ g0, const T* __restrict__ g1, T* s0,
                                  T* s1, int L, bool reverse) {
-  for (int k = threadIdx.x; k < L; k += NT) {
+  for (int k = threadIdx.x; k < L; k += blockDim.x) {
     const int j = reverse ? L - 1 - k : k;
     s0[k] = g0[j];
     s1[k] = g1[j];
@@ -535,9 +535,11 @@ __device__ inline void store_bands(S* drow, S* arow, T* lds, int o, int no, cons
 // ------------------------------------------------------------------ analysis chain
 // One workgroup per row (grid = rows), or, in split mode (levels == 1), `split` chunks of
 // CO outputs per workgroup (grid = rows * workgroups_per_row).
-template <typename S, typename T, int LT>
-__global__ void __launch_bounds__(NT) analysis_chain_kernel(AChainArgs args, int64_t rows,
-                                                            int wg_per_row) {
+template <typename S, typename T, int LT, int NTK>
+__global__ void __launch_bounds__(NTK) analysis_chain_kernel(AChainArgs args, int64_t rows,
+                                                             int wg_per_row) {
+  constexpr int NT = NTK;            // threads per workgroup: 512, or 128 for short rows
+  constexpr int CO = NT * VA * GA;   // outputs per level-0 chunk
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* const A = reinterpret_cast<T*>(smem_raw);
   T* const B = A + args.capA;
@@ -1189,8 +1191,9 @@ __device__ inline T fold_parked(const T* __restrict__ E, int i, int m, int md, i
 // VR consecutive coefficient pairs (2 VR positions) at a time from register windows of both
 // bands; positions away from the row ends go straight to the next low band (LDS) or to the
 // output row, the others are parked and folded after a barrier by one lane per fold target.
-template <typename S, typename T, int LT, bool PRE>
-__global__ void __launch_bounds__(NT) synthesis_rows_kernel(SynArgs) {
+template <typename S, typename T, int LT, bool PRE, int NTK>
+__global__ void __launch_bounds__(NTK) synthesis_rows_kernel(SynArgs) {
+  constexpr int NT = NTK;  // threads per workgroup: 512, or 128 for short rows
   extern __shared__ __align__(16) unsigned char smem_raw[];
   // the arguments, read in place through the kernel-argument segment pointer: scalar loads at
   // any (wave-uniform) offset, and never a private copy.  (The host compilation pass only
@@ -1456,12 +1459,14 @@ inline bool allow_full_lds(K kernel) {
 }
 
 template <typename S, typename T, int LT>
-int launch_achain(const AChainArgs& a, int64_t rows, int wg_per_row, size_t lds,
+int launch_achain(const AChainArgs& a, int64_t rows, int wg_per_row, size_t lds, int nt,
                   hipStream_t st) {
-  auto k = analysis_chain_kernel<S, T, LT>;
-  static const bool lds_ok = allow_full_lds(k);
+  auto k = nt == 128 ? analysis_chain_kernel<S, T, LT, 128> : analysis_chain_kernel<S, T, LT, 512>;
+  static const bool lds_ok =
+      allow_full_lds(analysis_chain_kernel<S, T, LT, 128>) &&
+      allow_full_lds(analysis_chain_kernel<S, T, LT, 512>);
   (void)lds_ok;
-  hipLaunchKernelGGL(k, dim3((unsigned)(rows * wg_per_row)), dim3(NT), lds, st, a, rows,
+  hipLaunchKernelGGL(k, dim3((unsigned)(rows * wg_per_row)), dim3(nt), lds, st, a, rows,
                      wg_per_row);
   FDWT_CHECK_LAUNCH();
   return 0;
@@ -1500,10 +1505,10 @@ inline int device_cus() {
 // occupancy at this LDS size), then evened out so that every workgroup gets the same number
 // of rows (the last one possibly fewer).
 template <typename K>
-inline int64_t persistent_grid(K kernel, size_t lds, int64_t rows) {
+inline int64_t persistent_grid(K kernel, int nt, size_t lds, int64_t rows) {
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
-                                                   NT, lds) != hipSuccess ||
+                                                   nt, lds) != hipSuccess ||
       per_cu < 1)
     per_cu = 1;
   const int64_t full = (int64_t)per_cu * device_cus();
@@ -1513,13 +1518,18 @@ inline int64_t persistent_grid(K kernel, size_t lds, int64_t rows) {
 }
 
 template <typename S, typename T, int LT>
-int launch_rchain(const SynArgs& a, size_t lds, hipStream_t st) {
-  static const bool lds_ok = allow_full_lds(synthesis_rows_kernel<S, T, LT, true>) &&
-                             allow_full_lds(synthesis_rows_kernel<S, T, LT, false>);
+int launch_rchain(const SynArgs& a, size_t lds, int nt, hipStream_t st) {
+  static const bool lds_ok = allow_full_lds(synthesis_rows_kernel<S, T, LT, true, 512>) &&
+                             allow_full_lds(synthesis_rows_kernel<S, T, LT, false, 512>) &&
+                             allow_full_lds(synthesis_rows_kernel<S, T, LT, true, 128>) &&
+                             allow_full_lds(synthesis_rows_kernel<S, T, LT, false, 128>);
   (void)lds_ok;
-  auto k = a.prefetch ? synthesis_rows_kernel<S, T, LT, true> : synthesis_rows_kernel<S, T, LT, false>;
-  const int64_t grid = persistent_grid(k, lds, a.rows);
-  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(NT), lds, st, a);
+  auto k = nt == 128 ? (a.prefetch ? synthesis_rows_kernel<S, T, LT, true, 128>
+                                   : synthesis_rows_kernel<S, T, LT, false, 128>)
+                     : (a.prefetch ? synthesis_rows_kernel<S, T, LT, true, 512>
+                                   : synthesis_rows_kernel<S, T, LT, false, 512>);
+  const int64_t grid = persistent_grid(k, nt, lds, a.rows);
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(nt), lds, st, a);
   FDWT_CHECK_LAUNCH();
   return 0;
 }
@@ -1546,10 +1556,10 @@ int launch_rchain(const SynArgs& a, size_t lds, hipStream_t st) {
   }
 
 template <typename S>
-int run_achain(const AChainArgs& a, int64_t rows, int wg, size_t lds, hipStream_t st,
+int run_achain(const AChainArgs& a, int64_t rows, int wg, size_t lds, int nt, hipStream_t st,
                bool templated) {
-  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_achain, a, rows, wg, lds, st) }
-  return launch_achain<S, float, 0>(a, rows, wg, lds, st);
+  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_achain, a, rows, wg, lds, nt, st) }
+  return launch_achain<S, float, 0>(a, rows, wg, lds, nt, st);
 }
 
 template <typename S>
@@ -1560,30 +1570,30 @@ int run_schain(const SChainArgs& a, int64_t rows, int wg, size_t lds, hipStream_
 }
 
 template <typename S>
-int run_rchain(const SynArgs& a, size_t lds, hipStream_t st, bool templated) {
-  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_rchain, a, lds, st) }
-  return launch_rchain<S, float, 0>(a, lds, st);
+int run_rchain(const SynArgs& a, size_t lds, int nt, hipStream_t st, bool templated) {
+  if (templated) { FDWT_TAPS_SWITCH(a.taps, launch_rchain, a, lds, nt, st) }
+  return launch_rchain<S, float, 0>(a, lds, nt, st);
 }
 
-int dispatch_rchain(const SynArgs& a, size_t lds, int dtype, hipStream_t st) {
+int dispatch_rchain(const SynArgs& a, size_t lds, int nt, int dtype, hipStream_t st) {
   const bool templ = a.taps <= MAXL_T;
   switch (dtype) {
-    case FDWT_F32: return run_rchain<float>(a, lds, st, templ);
-    case FDWT_F16: return run_rchain<__half>(a, lds, st, templ);
-    case FDWT_BF16: return run_rchain<bf16_t>(a, lds, st, templ);
-    case FDWT_F64: return launch_rchain<double, double, 0>(a, lds, st);
+    case FDWT_F32: return run_rchain<float>(a, lds, nt, st, templ);
+    case FDWT_F16: return run_rchain<__half>(a, lds, nt, st, templ);
+    case FDWT_BF16: return run_rchain<bf16_t>(a, lds, nt, st, templ);
+    case FDWT_F64: return launch_rchain<double, double, 0>(a, lds, nt, st);
     default: return FDWT_ERR_ARG;
   }
 }
 
-int dispatch_achain(const AChainArgs& a, int64_t rows, int wg, size_t lds, int dtype,
+int dispatch_achain(const AChainArgs& a, int64_t rows, int wg, size_t lds, int nt, int dtype,
                     hipStream_t st) {
   const bool templ = a.taps <= MAXL_T;
   switch (dtype) {
-    case FDWT_F32: return run_achain<float>(a, rows, wg, lds, st, templ);
-    case FDWT_F16: return run_achain<__half>(a, rows, wg, lds, st, templ);
-    case FDWT_BF16: return run_achain<bf16_t>(a, rows, wg, lds, st, templ);
-    case FDWT_F64: return launch_achain<double, double, 0>(a, rows, wg, lds, st);
+    case FDWT_F32: return run_achain<float>(a, rows, wg, lds, nt, st, templ);
+    case FDWT_F16: return run_achain<__half>(a, rows, wg, lds, nt, st, templ);
+    case FDWT_BF16: return run_achain<bf16_t>(a, rows, wg, lds, nt, st, templ);
+    case FDWT_F64: return launch_achain<double, double, 0>(a, rows, wg, lds, nt, st);
     default: return FDWT_ERR_ARG;
   }
 }
@@ -1609,11 +1619,11 @@ inline bool valid_common(int64_t rows, int taps, int mode, int dtype) {
 
 // LDS layout of an analysis chain: A holds the inputs of odd levels, B the staging window of
 // level 0 and the inputs of even levels >= 2; sizes in compute elements.
-void achain_caps(const int64_t* n_in, const int64_t* n_out, int levels, int L, int* capA,
-                 int* capB) {
-  // the level-0 window is staged in aligned groups of four: up to three elements before B
-  // (the last four elements of A are a guard) and three after the window
-  const int64_t stage = 2 * (int64_t)CO + (L > MAXL_T ? L : MAXL_T) - 2 + 4;
+void achain_caps(const int64_t* n_in, const int64_t* n_out, int levels, int L, int co,
+                 int* capA, int* capB) {
+  // the level-0 window (chunks of co outputs) is staged in aligned groups of four: up to
+  // three elements before B (the last four elements of A are a guard) and three after it
+  const int64_t stage = 2 * (int64_t)co + (L > MAXL_T ? L : MAXL_T) - 2 + 4;
   int64_t a = 0, b = stage;
   for (int l = 1; l < levels; ++l) {
     const int64_t need = std::max<int64_t>(2 * n_out[l] + L, n_in[l] + L) + 2;
@@ -1707,8 +1717,12 @@ extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* ap
   a.mode = mode;  // normalised per level in the kernel (reflect on one sample)
   a.off = off;
   if (off < 0 || off > taps) return FDWT_ERR_ARG;
+  // short rows: 128-thread workgroups (chunks of 512 outputs) keep the threads busy and
+  // let four times as many rows share a CU
+  const int nt = n_out[0] <= 3 * 128 * VA * GA ? 128 : NT;
+  const int co = nt * VA * GA;
   int capA, capB;
-  achain_caps(n_in, n_out, levels, taps, &capA, &capB);
+  achain_caps(n_in, n_out, levels, taps, co, &capA, &capB);
   a.capA = capA;
   a.capB = capB;
   const int cs = compute_size(dtype);
@@ -1716,7 +1730,7 @@ extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* ap
   if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
   int wg = 1;
   a.split = 0;
-  const int64_t nchunks = cdiv(n_out[0], CO);
+  const int64_t nchunks = cdiv(n_out[0], co);
   if (levels == 1 && rows < 1024 && nchunks > 1) {
     // few long rows: spread the chunks of a row over several workgroups
     const int64_t want = cdiv(2048, rows);
@@ -1724,7 +1738,7 @@ extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* ap
     wg = (int)cdiv(nchunks, a.split);
   }
   if (rows * wg > INT32_MAX) return FDWT_ERR_ARG;
-  return dispatch_achain(a, rows, wg, lds, dtype, static_cast<hipStream_t>(stream));
+  return dispatch_achain(a, rows, wg, lds, nt, dtype, static_cast<hipStream_t>(stream));
 }
 
 // Whole-row synthesis chain: LDS layout, level records and prefetch jobs, launch.
@@ -1779,8 +1793,11 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
     r.nva = l > 0 ? s.nc[l] : (s.approx ? s.nc[0] : 0);
     r.nvd = s.details[l] ? s.nc[l] : 0;
   }
+  // threads per workgroup: 128 for short rows (the last level's pairs in at most three passes
+  // of 128 threads), else 512
+  const int nt = geo[J - 1].vend - geo[J - 1].vbeg <= 3 * 128 * VR ? 128 : 512;
   const bool pre = syn_regs(
-      J, s.nc, s.approx, s.details, ZL, (int)yP, (int)yQ, (int)yD,
+      J, s.nc, s.approx, s.details, ZL, (int)yP, (int)yQ, (int)yD, nt,
       [&](bool tail, int k, int c0, int cnt, int dest, int l, bool is_approx) {
         const void* band = is_approx ? s.approx : s.details[l];
         const int es = dtype_size(dtype);
@@ -1809,7 +1826,7 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
   a.prefetch = pre ? 1 : 0;
   a.offE = (int32_t)yE;
   a.offTap = (int32_t)yT;
-  return dispatch_rchain(a, lds, dtype, st);
+  return dispatch_rchain(a, lds, nt, dtype, st);
 }
 
 extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* details, void* out,
