@@ -36,6 +36,7 @@ extern "C" {
 
 #define FDWT_ERR_ARG (-1)         /* invalid size / mode / dtype / null pointer */
 #define FDWT_ERR_TOO_LONG (-2)    /* a row does not fit the kernel's on-chip buffers */
+#define FDWT_ERR_SCRATCH (-3)    /* a call needs more than the fixed scratch of a no-allocation entry */
 #define FDWT_MAX_LEVELS 32
 #define FDWT_SYN_MAX_LEVELS 16   /* levels per fdwt_synthesis_chain call */
 
@@ -172,6 +173,22 @@ int fdwt_morlet_backward_h(const void* x, const void* g, void* workspace,
                            const int32_t* support, const int32_t* chan, int32_t dil,
                            int32_t channels, int32_t g_scales, int32_t accumulate,
                            int32_t dtype, void* stream);
+
+/* No counterpart in the reference: fdwt_morlet_backward_h for callers that cannot allocate
+ * (code under HIP graph capture, allocation-free serving loops).  Same arguments without the
+ * workspace, same kernels and result bit for bit; the partial sums go to a fixed array of
+ * fdwt_morlet_backward_h_noalloc_capacity() bytes (32 MiB) in device memory, one per GPU,
+ * held until the process ends.  A call whose partial sums do not fit returns FDWT_ERR_SCRATCH
+ * before any launch (the matrix-core path needs resident-workgroups x n_scales x K x channels
+ * elements, the vector path, K > 128, rows x ceil(n_out / 512) x the same).  All calls on one
+ * GPU share that array: calls that overlap on one GPU (several streams or threads) race. */
+int64_t fdwt_morlet_backward_h_noalloc_capacity(void);
+int fdwt_morlet_backward_h_noalloc(const void* x, const void* g, void* gh, int64_t rows,
+                                   int64_t n_in, int64_t n_out, int64_t x_off,
+                                   int32_t n_scales, int32_t half, const int32_t* support,
+                                   const int32_t* chan, int32_t dil, int32_t channels,
+                                   int32_t g_scales, int32_t accumulate, int32_t dtype,
+                                   void* stream);
 
 /* Fused scalogram mix, replacing `mix_forward` / `mix_backward` (src/fdwt/kernels/mix.py:74-108):
  *   forward   y[r, n] (+)= sum_s a[d, chan[s]] |W_s| + b[d, chan[s]] Re W_s,  d = (r + row0) % d_dim

@@ -20,6 +20,7 @@ _LIB = None
 
 DTYPE = {torch.float32: 0, torch.float64: 1, torch.float16: 2, torch.bfloat16: 3}
 ERR_TOO_LONG = -2
+ERR_SCRATCH = -3
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -48,6 +49,9 @@ SIGNATURES = {
     "fdwt_morlet_backward_h_workspace": [_I64, _I64, _I32, _I32, _I32],
     "fdwt_morlet_backward_h": [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _I32, _PI32,
                                _PI32, _I32, _I32, _I32, _I32, _I32, _P],
+    "fdwt_morlet_backward_h_noalloc_capacity": [],
+    "fdwt_morlet_backward_h_noalloc": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _PI32,
+                                       _PI32, _I32, _I32, _I32, _I32, _I32, _P],
     "fdwt_mix_workspace": [_I64, _I64, _I32],
     "fdwt_mix_forward": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _PI32, _PI32,
                          _I32, _I32, _I32, _I32, _I64, _I32, _I32, _P],
@@ -66,6 +70,7 @@ SIGNATURES = {
 _RESTYPE = {"fdwt_error_string": ctypes.c_char_p, "fdwt_version": ctypes.c_char_p,
             "fdwt_chain_max_length": ctypes.c_int64,
             "fdwt_morlet_backward_h_workspace": ctypes.c_int64,
+            "fdwt_morlet_backward_h_noalloc_capacity": ctypes.c_int64,
             "fdwt_mix_workspace": ctypes.c_int64, "fdwt_softmax_workspace": ctypes.c_int64}
 
 

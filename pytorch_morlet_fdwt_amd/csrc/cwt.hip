@@ -19,6 +19,7 @@
 // words (no bank conflicts) and every output store is coalesced.  Scales are processed in
 // groups of SG with 2 V SG accumulators in registers.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1498,21 +1499,21 @@ extern "C" int64_t fdwt_morlet_backward_h_workspace(int64_t rows, int64_t n_out,
   return rows * tiles * (int64_t)n_scales * (2 * (int64_t)half + 1) * channels;
 }
 
-extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* workspace,
-                                      int64_t workspace_elems, void* gh, int64_t rows,
-                                      int64_t n_in, int64_t n_out, int64_t x_off,
-                                      int32_t n_scales, int32_t half, const int32_t* support,
-                                      const int32_t* chan, int32_t dil, int32_t channels,
-                                      int32_t g_scales, int32_t accumulate, int32_t dtype,
-                                      void* stream) {
+// The filter gradient with a workspace of workspace_elems elements.  The columns written are
+// those of the path taken (resident workgroups on the matrix cores, rows x tiles on the
+// vector kernel); a workspace smaller than that returns FDWT_ERR_SCRATCH before any launch.
+static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
+                                 int64_t workspace_elems, void* gh, int64_t rows, int64_t n_in,
+                                 int64_t n_out, int64_t x_off, int32_t n_scales, int32_t half,
+                                 const int32_t* support, const int32_t* chan, int32_t dil,
+                                 int32_t channels, int32_t g_scales, int32_t accumulate,
+                                 int32_t dtype, void* stream) {
   Stage st;
   int e = fill_stage(st, x, g, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
   if (e) return e;
   if (!workspace || !gh || rows < 0 || (dtype != FDWT_F32 && dtype != FDWT_F64)) return FDWT_ERR_ARG;
   for (int s = 0; s < n_scales; ++s)
     if (chan[s] >= g_scales) return FDWT_ERR_ARG;
-  const int64_t need = fdwt_morlet_backward_h_workspace(rows, n_out, n_scales, half, channels);
-  if (workspace_elems < need) return FDWT_ERR_ARG;
   const int64_t K = 2 * (int64_t)half + 1;
   const int64_t n_el = n_scales * K * channels;
   if (rows == 0 || n_out == 0) return 0;
@@ -1535,6 +1536,7 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
     auto k = morlet_grad_h_mfma_kernel<TYPE, CPLX, N>;                                        \
     FDWT_LDS_ONCE(k);                                                                         \
     ncols = resident_blocks(k, mlds, total);                                                  \
+    if ((int64_t)ncols * n_el > workspace_elems) return FDWT_ERR_SCRATCH;                     \
     for (int s0 = 0; s0 < n_scales && !rc; s0 += grp)                                         \
       rc = launch(k, ncols, mlds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,    \
                   tiles, total, s0, std::min(n_scales, s0 + grp), sk);                        \
@@ -1563,6 +1565,7 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
   const size_t lds = (size_t)(HPAD + ((span + 4 + 3) & ~3) + (int64_t)HS4 * TT * channels) * cs;
   const int64_t blocks = rows * tiles;
   if (n_el > INT32_MAX) return FDWT_ERR_ARG;
+  if (blocks * n_el > workspace_elems) return FDWT_ERR_SCRATCH;
   if (dil != 1 && dil != 2 && dil % 4 != 0) return FDWT_ERR_ARG;
   // scales [0, n4) in groups of 4; the remaining 1 or 2 in one smaller group (3 stay in a
   // group of 4, one slot idle)
@@ -1601,6 +1604,69 @@ extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* worksp
 #undef BWH
 #undef BWH_DIL
 #undef BWH_HS
+}
+
+extern "C" int fdwt_morlet_backward_h(const void* x, const void* g, void* workspace,
+                                      int64_t workspace_elems, void* gh, int64_t rows,
+                                      int64_t n_in, int64_t n_out, int64_t x_off,
+                                      int32_t n_scales, int32_t half, const int32_t* support,
+                                      const int32_t* chan, int32_t dil, int32_t channels,
+                                      int32_t g_scales, int32_t accumulate, int32_t dtype,
+                                      void* stream) {
+  if (rows < 0 || n_out < 0 || n_scales < 0 || half < 0 || channels < 1) return FDWT_ERR_ARG;
+  const int64_t need = fdwt_morlet_backward_h_workspace(rows, n_out, n_scales, half, channels);
+  if (workspace_elems < need) return FDWT_ERR_ARG;
+  return morlet_backward_h_run(x, g, workspace, workspace_elems, gh, rows, n_in, n_out, x_off,
+                               n_scales, half, support, chan, dil, channels, g_scales,
+                               accumulate, dtype, stream);
+}
+
+// ------------------------------------------------------------------ no-allocation variant
+// The filter gradient's partial sums in a fixed device array instead of a caller workspace.
+// Host code never passes the array's name to a kernel: its device address is resolved once
+// per device (hipGetSymbolAddress, with that device current) and kept in noalloc_ptr.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = 32ll << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::once_flag noalloc_once[NOALLOC_MAX_DEVICES];
+void* noalloc_ptr[NOALLOC_MAX_DEVICES];
+hipError_t noalloc_err[NOALLOC_MAX_DEVICES];
+
+// device address of the current device's copy of `scratch`
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return FDWT_ERR_ARG;
+  std::call_once(noalloc_once[dev], [dev] {
+    noalloc_err[dev] = hipGetSymbolAddress(&noalloc_ptr[dev], HIP_SYMBOL(scratch));
+  });
+  if (noalloc_err[dev] != hipSuccess) return (int)noalloc_err[dev];
+  if (!noalloc_ptr[dev]) return FDWT_ERR_ARG;
+  *out = noalloc_ptr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int64_t fdwt_morlet_backward_h_noalloc_capacity(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int fdwt_morlet_backward_h_noalloc(const void* x, const void* g, void* gh,
+                                              int64_t rows, int64_t n_in, int64_t n_out,
+                                              int64_t x_off, int32_t n_scales, int32_t half,
+                                              const int32_t* support, const int32_t* chan,
+                                              int32_t dil, int32_t channels, int32_t g_scales,
+                                              int32_t accumulate, int32_t dtype, void* stream) {
+  if (dtype != FDWT_F32 && dtype != FDWT_F64) return FDWT_ERR_ARG;
+  void* ws = nullptr;
+  const int e = noalloc_scratch(&ws);
+  if (e) return e;
+  // every column the kernels read back is written first by the same call: nothing to clear
+  const int64_t elems = NOALLOC_SCRATCH_BYTES / (dtype == FDWT_F64 ? 8 : 4);
+  return morlet_backward_h_run(x, g, ws, elems, gh, rows, n_in, n_out, x_off, n_scales, half,
+                               support, chan, dil, channels, g_scales, accumulate, dtype,
+                               stream);
 }
 
 extern "C" int64_t fdwt_mix_workspace(int64_t rows, int64_t n_out, int32_t n_scales) {
