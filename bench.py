@@ -263,6 +263,24 @@ def _timed(step, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def _graph_timed(step, steps):
+    """Mean ms per replay of ``step`` captured in one HIP graph.  The warm-up runs on the
+    capture's side stream and no autograd graph from before the capture is alive, so every
+    node the capture reaches was made on the capturing stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    return _timed(g.replay, steps, 2)
+
+
 def _cpu_median(run, reps=3):
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -298,7 +316,8 @@ def dwt_cfg1(steps, warmup, dev, cpu):
     import pytorch_morlet_fdwt_amd as fdwt
     x = torch.randn(*DWT1_SHAPE, DWT1_N, generator=torch.Generator().manual_seed(0))
     xd = x.to(dev).requires_grad_()
-    y0 = fdwt.waverec(fdwt.wavedec(xd, "db4", "symmetric", DWT1_LEVEL), "db4", "symmetric")
+    with torch.no_grad():  # the output shape only: no autograd graph is kept
+        y0 = fdwt.waverec(fdwt.wavedec(xd, "db4", "symmetric", DWT1_LEVEL), "db4", "symmetric")
     gy = torch.randn(y0.shape, generator=torch.Generator().manual_seed(1)).to(dev)
 
     def step():
@@ -306,6 +325,7 @@ def dwt_cfg1(steps, warmup, dev, cpu):
         torch.autograd.grad(y, xd, gy)
 
     ms = _timed(step, steps, warmup)
+    gms = _graph_timed(step, steps)
     R = DWT1_SHAPE[0] * DWT1_SHAPE[1]
     lens = coeff_lengths(DWT1_N, 8, "symmetric", DWT1_LEVEL)
     C = sum(lens) + lens[-1]
@@ -316,6 +336,9 @@ def dwt_cfg1(steps, warmup, dev, cpu):
            "samples_per_s": R * DWT1_N / (ms * 1e-3),
            "config": {"workload": "BASELINE configs[0]: db4, symmetric, level 5, x fp32 "
                                   "(32,64,2500), waverec(wavedec(x)) fwd+bwd"},
+           "graph": {"ms_per_step": gms, "value": byts / (gms * 1e-3) / 1e9,
+                     "note": "the same step captured once in a HIP graph (torch.cuda.graph) "
+                             "and replayed: kernel time without the host's launch work"},
            "roofline": {"bound": "hbm", "achieved": byts / (ms * 1e-3) / 1e9,
                         "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                         "frac": byts / (ms * 1e-3) / HBM_PEAK, "alg_bytes": byts}}

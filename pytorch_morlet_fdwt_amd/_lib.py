@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from functools import lru_cache
 
 import torch
 
@@ -161,8 +162,11 @@ def require_gpu(*tensors):
                 f"tensors only; got a tensor on {t.device}")
 
 
-def stream(device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+def stream(device) -> int:
+    """torch's current stream on ``device`` as a raw hipStream_t (an int for the c_void_p
+    argument): inside torch.cuda.graph capture this is the capturing stream."""
+    idx = device.index if isinstance(device, torch.device) else device
+    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if idx is None else idx)
 
 
 def ptr(t) -> ctypes.c_void_p:
@@ -175,6 +179,15 @@ def ptr_array(tensors):
 
 
 def i64_array(values):
+    """A C int64 array of ``values``; arrays of tuples are built once and shared (the entry
+    points only read them)."""
+    if isinstance(values, tuple):
+        return _i64_tuple(values)
+    return (ctypes.c_int64 * max(1, len(values)))(*[int(v) for v in values])
+
+
+@lru_cache(maxsize=4096)
+def _i64_tuple(values: tuple):
     return (ctypes.c_int64 * max(1, len(values)))(*[int(v) for v in values])
 
 

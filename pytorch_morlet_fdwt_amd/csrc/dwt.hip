@@ -533,12 +533,17 @@ __device__ inline void store_bands(S* drow, S* arow, T* lds, int o, int no, cons
 }
 
 // ------------------------------------------------------------------ analysis chain
+// Thread groups per level-0 chunk: 128-thread workgroups (short rows) take a row of up to
+// 1280 outputs in one chunk, so all of its loads are in flight at once.
+constexpr int achain_groups(int nt) { return nt == 128 ? 5 : GA; }
+
 // One workgroup per row (grid = rows), or, in split mode (levels == 1), `split` chunks of
 // CO outputs per workgroup (grid = rows * workgroups_per_row).
 template <typename S, typename T, int LT, int NTK>
 __global__ void __launch_bounds__(NTK) analysis_chain_kernel(AChainArgs args, int64_t rows,
                                                              int wg_per_row) {
   constexpr int NT = NTK;            // threads per workgroup: 512, or 128 for short rows
+  constexpr int GA = achain_groups(NTK);
   constexpr int CO = NT * VA * GA;   // outputs per level-0 chunk
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* const A = reinterpret_cast<T*>(smem_raw);
@@ -1717,10 +1722,10 @@ extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* ap
   a.mode = mode;  // normalised per level in the kernel (reflect on one sample)
   a.off = off;
   if (off < 0 || off > taps) return FDWT_ERR_ARG;
-  // short rows: 128-thread workgroups (chunks of 512 outputs) keep the threads busy and
-  // let four times as many rows share a CU
+  // short rows: 128-thread workgroups (one chunk of up to 1280 outputs) keep the threads
+  // busy and let four times as many rows share a CU
   const int nt = n_out[0] <= 3 * 128 * VA * GA ? 128 : NT;
-  const int co = nt * VA * GA;
+  const int co = nt * VA * achain_groups(nt);
   int capA, capB;
   achain_caps(n_in, n_out, levels, taps, co, &capA, &capB);
   a.capA = capA;

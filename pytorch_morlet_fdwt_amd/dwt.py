@@ -76,6 +76,7 @@ def _synthesis(a2, d2, h0, h1, mode, off, n, R, dtype, device):
 
 
 @functools.lru_cache(maxsize=None)
+@functools.lru_cache(maxsize=None)
 def _chain_max(taps: int, dtype) -> int:
     return _lib.lib().fdwt_chain_max_length(taps, _lib.dtype_code(dtype))
 
