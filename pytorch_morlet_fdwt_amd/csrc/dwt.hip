@@ -84,8 +84,10 @@ struct SChainArgs {
 // The whole-row synthesis kernel (one workgroup per row at a time, rows blockIdx.x,
 // blockIdx.x + gridDim.x, ...) keeps the low band of every level in LDS and reads each band of
 // a row from HBM exactly once, into prefetch registers, well before it is used.  A prefetch
-// register holds up to NT consecutive coefficients of one band (lane t the t-th of them).  Two
-// register sets:
+// register holds up to PQ NT consecutive coefficients of one band (lane t the coefficients
+// t + j NT, j < PQ: every load and LDS store of the register is coalesced), loaded through a
+// buffer resource whose range is the register's coefficients (lanes past the end read 0), so a
+// register costs one descriptor read and no per-lane address arithmetic.  Two register sets:
 //  * the head (PA registers): every band of the levels before the last (a_0, d_0 .. d_{J-2}),
 //    requested for the next row just before the current row's last level runs;
 //  * the tail (PB registers): the last level's band(s), requested at the start of the row, so
@@ -94,8 +96,11 @@ struct SChainArgs {
 // the start of its last level); in between, staging reads registers whose loads are known to
 // be complete, so the compiler adds no wait of its own.  Rows whose bands do not fit the sets
 // load each band at its level instead (no prefetch).
-constexpr int PA = 24;  // head prefetch registers per thread
-constexpr int PB = 20;  // tail prefetch registers per thread
+constexpr int PQ = 4;  // coefficients per lane in one prefetch register
+constexpr int PA = 9;  // head prefetch registers per thread (2- and 4-byte bands)
+constexpr int PB = 5;  // tail prefetch registers per thread
+// head registers for bands of es-byte coefficients (8-byte ones take twice the VGPRs)
+__host__ __device__ constexpr int syn_pa(int es) { return es == 8 ? 6 : PA; }
 
 // LDS buffers of the whole-row synthesis kernel, in this order (element offsets P, Q, D, E,
 // T): the low band of level l lives in P when J - 1 - l is even and in Q otherwise (the last
@@ -192,6 +197,7 @@ struct SynTab {
   SynLoad ldB[PB];  // tail registers
   uint32_t stA[PA];
   uint32_t stB[PB];
+  uint32_t stpad[2];
 };
 static_assert(sizeof(SynTab) % 16 == 0, "the LDS copy uses whole 16-byte words");
 
@@ -212,12 +218,13 @@ struct SynArgs {
 };
 
 // The prefetch registers of a row: each band of the head (a_0, d_0 .. d_{J-2} when J > 1)
-// and of the tail (d_{J-1}, or a_0 and d_0 when J == 1) takes ceil(count / NT) registers of
-// its set.  emit(tail, k, c0, cnt, dest, level, is_approx) is called for each register;
-// returns false when a set overflows (then nothing is prefetched).
+// and of the tail (d_{J-1}, or a_0 and d_0 when J == 1) takes ceil(count / per) registers of
+// its set (per = PQ NT coefficients; pa, pb registers in the sets).  emit(tail, k, c0, cnt,
+// dest, level, is_approx) is called for each register; returns false when a set overflows
+// (then nothing is prefetched).
 template <typename F>
 inline bool syn_regs(int J, const int32_t* nc, const void* approx, const void* const* details,
-                     int ZL, int yP, int yQ, int yD, int nt, F&& emit) {
+                     int ZL, int yP, int yQ, int yD, int per, int pa, int pb, F&& emit) {
   int ka = 0, kb = 0;
   for (int s = 0; s <= J; ++s) {
     const int l = s == 0 ? 0 : s - 1;
@@ -226,10 +233,10 @@ inline bool syn_regs(int J, const int32_t* nc, const void* approx, const void* c
     if (!ptr || cnt <= 0) continue;
     const bool tail = l == J - 1;
     const int dest = (s == 0 ? syn_src(0, J, yP, yQ) : syn_dbuf(l, J, yQ, yD)) + ZL;
-    for (int c0 = 0; c0 < cnt; c0 += nt) {
+    for (int c0 = 0; c0 < cnt; c0 += per) {
       int& k = tail ? kb : ka;
-      if (k == (tail ? PB : PA)) return false;
-      emit(tail, k, c0, cnt - c0 < nt ? cnt - c0 : nt, dest + c0, l, s == 0);
+      if (k == (tail ? pb : pa)) return false;
+      emit(tail, k, c0, cnt - c0 < per ? cnt - c0 : per, dest + c0, l, s == 0);
       ++k;
     }
   }
@@ -244,6 +251,23 @@ typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
 __device__ inline v4u_t global_load16(const float* p) {
   typedef __attribute__((address_space(1))) const v4u_t* gptr;
   return *(gptr)p;
+}
+
+// One coefficient through a buffer resource (0 outside its range), as raw storage bits.
+template <typename S>
+__device__ inline S buffer_load_raw(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  S v;
+  if constexpr (sizeof(S) == 2) {
+    const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    __builtin_memcpy(&v, &u, 2);
+  } else if constexpr (sizeof(S) == 4) {
+    const unsigned u = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    __builtin_memcpy(&v, &u, 4);
+  } else {
+    const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    __builtin_memcpy(&v, &u, 8);
+  }
+  return v;
 }
 
 template <typename S>
@@ -1251,27 +1275,31 @@ __global__ void __launch_bounds__(NTK) synthesis_rows_kernel(SynArgs) {
   __syncthreads();
 
   // ---- prefetch registers: raw band values, converted only when staged
-  S pa[PA], pb[PB];
+  constexpr int NPA = syn_pa((int)sizeof(S));
+  S pa[NPA][PQ], pb[PB][PQ];
 #pragma unroll
-  for (int k = 0; k < PA; ++k) pa[k] = S{};
+  for (int k = 0; k < NPA; ++k)
 #pragma unroll
-  for (int k = 0; k < PB; ++k) pb[k] = S{};
+    for (int j = 0; j < PQ; ++j) pa[k][j] = S{};
+#pragma unroll
+  for (int k = 0; k < PB; ++k)
+#pragma unroll
+    for (int j = 0; j < PQ; ++j) pb[k][j] = S{};
+  const int voff = tid * (int)sizeof(S);  // this lane's byte offset in a register's first NT
   // Load descriptors and staging words come from the LDS copy of the tables (every lane reads
-  // the same address); only a register's count needs to be wave-uniform (it guards the load).
+  // the same address) and are made wave-uniform, so the row address and the buffer range are
+  // scalar arithmetic; the loads take voff plus a constant per j.
   auto issue = [&](auto& regs, const SynLoad* t, int n, int64_t r) __attribute__((always_inline)) {
 #pragma unroll
-    for (int k0 = 0; k0 < n; k0 += 4) {
-      SynLoad d[4];
+    for (int k = 0; k < n; ++k) {
+      const SynLoad d = lds_uniform(t + k);
+      if (d.cnt > 0) {
+        char* base = const_cast<char*>(static_cast<const char*>(d.base)) + r * (int64_t)d.stride;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            base, (short)0, d.cnt * (int)sizeof(S), 0x00020000);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = t[k0 + i];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int cnt = __builtin_amdgcn_readfirstlane(d[i].cnt);
-        if (cnt > 0) {
-          const int e = tid < cnt ? tid : cnt - 1;
-          regs[k0 + i] = global_load(
-              reinterpret_cast<const S*>(static_cast<const char*>(d[i].base) + r * (int64_t)d[i].stride), e);
-        }
+        for (int j = 0; j < PQ; ++j)
+          regs[k][j] = buffer_load_raw<S>(rs, voff, j * NT * (int)sizeof(S));
       }
     }
   };
@@ -1279,22 +1307,25 @@ __global__ void __launch_bounds__(NTK) synthesis_rows_kernel(SynArgs) {
 #pragma unroll
     for (int k = 0; k < n; ++k) {
       if (mask & (1u << k)) {
-        const uint32_t w = t[k];
+        const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(t[k]);
         const int dest = (int)(w & 0x3ffffu), cnt = (int)(w >> 18);
-        if (tid < cnt) lds[dest + tid] = T(Storage<S>::load(&regs[k], 0));
+        T* const d = lds + dest + tid;
+#pragma unroll
+        for (int j = 0; j < PQ; ++j)
+          if (tid + j * NT < cnt) d[j * NT] = T(Storage<S>::load(&regs[k][j], 0));
       }
     }
   };
-  auto issue_head = [&](int64_t r) __attribute__((always_inline)) { issue(pa, tab->ldA, PA, r); };
+  auto issue_head = [&](int64_t r) __attribute__((always_inline)) { issue(pa, tab->ldA, NPA, r); };
   auto issue_tail = [&](int64_t r) __attribute__((always_inline)) { issue(pb, tab->ldB, PB, r); };
   auto stage_head = [&](int l) __attribute__((always_inline)) {
-    stage(pa, tab->stA, PA, (uint32_t)__builtin_amdgcn_readfirstlane(tab->maskA[l]));
+    stage(pa, tab->stA, NPA, (uint32_t)__builtin_amdgcn_readfirstlane(tab->maskA[l]));
   };
   auto stage_tail = [&]() __attribute__((always_inline)) {
     stage(pb, tab->stB, PB, (1u << PB) - 1u);
   };
   auto wait_loads = [&]() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
-  // without prefetch: the bands of level l, NT * PB coefficients at a time through pb
+  // without prefetch: the bands of level l, NT * PB * PQ coefficients at a time through pb
   auto direct = [&](int l, int64_t r) __attribute__((always_inline)) {
     const int src = __builtin_amdgcn_readfirstlane(tab->lv[l].src);
     const int dbuf = __builtin_amdgcn_readfirstlane(tab->lv[l].dbuf);
@@ -1304,17 +1335,18 @@ __global__ void __launch_bounds__(NTK) synthesis_rows_kernel(SynArgs) {
       if (!band) continue;
       const int cnt = args.nc[l];
       T* dstp = lds + (s == 0 ? src : dbuf) + ZL;
-      for (int c0 = 0; c0 < cnt; c0 += NT * PB) {
+      for (int c0 = 0; c0 < cnt; c0 += NT * PB * PQ) {
 #pragma unroll
-        for (int k = 0; k < PB; ++k) {
+        for (int k = 0; k < PB * PQ; ++k) {
           const int c = c0 + k * NT + tid;
-          if (c0 + k * NT < cnt) pb[k] = global_load(band, r * (int64_t)cnt + (c < cnt ? c : cnt - 1));
+          if (c0 + k * NT < cnt)
+            pb[k / PQ][k % PQ] = global_load(band, r * (int64_t)cnt + (c < cnt ? c : cnt - 1));
         }
         wait_loads();
 #pragma unroll
-        for (int k = 0; k < PB; ++k) {
+        for (int k = 0; k < PB * PQ; ++k) {
           const int c = c0 + k * NT + tid;
-          if (c < cnt) dstp[c] = T(Storage<S>::load(pb + k, 0));
+          if (c < cnt) dstp[c] = T(Storage<S>::load(&pb[k / PQ][k % PQ], 0));
         }
       }
     }
@@ -1802,7 +1834,8 @@ int synthesis_rows(const SChainArgs& s, int64_t rows, int dtype, hipStream_t st)
   // of 128 threads), else 512
   const int nt = geo[J - 1].vend - geo[J - 1].vbeg <= 3 * 128 * VR ? 128 : 512;
   const bool pre = syn_regs(
-      J, s.nc, s.approx, s.details, ZL, (int)yP, (int)yQ, (int)yD, nt,
+      J, s.nc, s.approx, s.details, ZL, (int)yP, (int)yQ, (int)yD, PQ * nt,
+      syn_pa(dtype_size(dtype)), PB,
       [&](bool tail, int k, int c0, int cnt, int dest, int l, bool is_approx) {
         const void* band = is_approx ? s.approx : s.details[l];
         const int es = dtype_size(dtype);
