@@ -833,6 +833,179 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
   }
 }
 
+// ------------------------------------------------------------------ bank adjoint, matrix cores
+// The adjoint as a matrix product.  Positions p = lo + rho + dil i (residue rho < dil) of a
+// row see g only at q = lo - x_off + rho + dil j, so with
+//     u_{rho,s,c}[j] = g[r, chan_s, lo - x_off + rho + dil j, c]   (0 outside [0, n_out))
+// and the full filters F_{s,c}[k], |k| <= sup_s (F_{s,0}[k] = taps[s][|k|][0] and F_{s,1}[k] =
+// sign(k) taps[s][|k|][1]: the even and odd Morlet halves of the compact taps)
+//     gx[r, lo + rho + dil i] = sum_{s,c} sum_k F_{s,c}[k] u_{rho,s,c}[i + k].
+// The filter does not depend on the row or the residue, so for 16 lines m = (row, residue) and
+// 16 consecutive i this is U (16 lines x 16 + 2 sup_s window positions) times the banded
+// Toeplitz matrix Z[j][i] = F[j - i - sup_s] (window x 16 outputs), accumulated over (s, c) in
+// the result registers of one v_mfma_*_16x16x4 per 4 window positions j = 4 t + kap (A: lane l
+// gives U[l % 16][4 t + l / 16]; B: Z[4 t + l / 16][l % 16]).  Z is the same for every tile,
+// so a wave reads it once per step for its MA_NB tiles.
+//
+// The 16 lines of a workgroup are 16 / D rows x D consecutive residues rho0 .. rho0 + D - 1
+// (D = min(dil, 16)), so a row's staged positions rho0 + rho + dil j are runs of D consecutive
+// g positions: whole cache lines from D = 16 on, one contiguous range for dil <= 16.  A
+// workgroup takes MA_TI = 4 MA_NB 16 consecutive i (MA_NB tiles per wave); consecutive
+// workgroups take consecutive residue blocks.  Per scale it stages u of both channels over the
+// tiles' window (MA_TI + 2 sup_s + 3 <= MA_WL positions; the last 3 meet only zero taps) in
+// LDS, lines WS words apart with WS = 4 (mod 32), so the 64 lanes of an A read (16 lines x 4
+// consecutive j) and of a staging store (D lines x 64 / D consecutive j) hit distinct banks;
+// and the scale's zero-padded filters.  The whole window of the next scale is loaded into
+// registers (MA_PFN loads per thread, through a buffer resource per (row, scale) plane:
+// positions outside [0, n_out), and rows past the last, read 0) while the current scale is
+// multiplied.
+constexpr int MA_NB = 2;               // 16 x 16 tiles per wave
+constexpr int MA_TI = 4 * 16 * MA_NB;  // outputs per line of a workgroup
+constexpr int MA_WL = 256;             // longest staged window (half <= (MA_WL - MA_TI - 3) / 2)
+constexpr int MA_PFN = 16 * MA_WL / NT;  // prefetch loads per thread (16 lines x MA_WL)
+
+// LDS line stride (elements) of the staged u and length of a filter table, for a stage's half
+__host__ __device__ inline int ma_ws(int half) { return 32 * ((MA_TI + 2 * half - 1 + 31) / 32) + 4; }
+__host__ __device__ inline int ma_fl(int half) { return 2 * half + 34; }
+
+// One g position (C values, re then im) through a buffer resource; 0 outside its range.
+template <typename T, int C>
+__device__ inline void ma_load(__amdgpu_buffer_rsrc_t r, int off, T (&v)[C]) {
+  if constexpr (sizeof(T) * C == 4) {
+    const unsigned u = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    __builtin_memcpy(v, &u, 4);
+  } else if constexpr (sizeof(T) * C == 8) {
+    const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    __builtin_memcpy(v, &u, 8);
+  } else {
+    const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    __builtin_memcpy(v, &u, 16);
+  }
+}
+
+template <typename T, bool CPLX, int D>
+__global__ void __launch_bounds__(NT) morlet_adjoint_mfma_kernel(Stage st, const T* __restrict__ g,
+                                                                 T* __restrict__ gx, int g_scales,
+                                                                 int64_t rows, int rblocks,
+                                                                 int itiles, int64_t lo,
+                                                                 int64_t hi, int accumulate) {
+  constexpr int C = CPLX ? 2 : 1;
+  constexpr int RW = 16 / D;            // rows of a workgroup
+  constexpr int LD = __builtin_ctz(D);
+  static_assert(MA_PFN % D == 0 && MA_PFN / D == RW, "D * MA_WL slots per row");
+  typedef typename Mfma16<T>::v4 v4;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int half = st.half, dil = st.dil;
+  const int WS = ma_ws(half), FL = ma_fl(half), PADL = half + 15;
+  T* const U = reinterpret_cast<T*>(smem_raw);  // [C][16][WS]
+  T* const Fz = U + C * 16 * WS;                // [C][FL]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t blk = blockIdx.x;
+  const int rb = (int)(blk % rblocks);
+  const int64_t rest = blk / rblocks;
+  const int it = (int)(rest % itiles);
+  const int64_t row0 = (rest / itiles) * RW;
+  const int rho0 = rb * D;
+  const int64_t i0 = (int64_t)it * MA_TI;
+  const T* taps = static_cast<const T*>(st.taps);
+
+  if (!accumulate) {  // zero the positions g does not reach, spread over the row group's blocks
+    const int64_t outside = lo + (st.n_in - hi);
+    const int64_t nb = (int64_t)itiles * rblocks, b = (int64_t)it * rblocks + rb;
+    for (int64_t e = b * NT + tid; e < RW * outside; e += nb * NT) {
+      const int64_t r = row0 + e / outside, j = e % outside;
+      if (r < rows) gx[r * st.n_in + (j < lo ? j : hi + (j - lo))] = T(0);
+    }
+  }
+
+  // staging slots: load m of a thread covers row m >> LD, flat index f = tid + NT (m & (D-1))
+  // of the row's D * MA_WL slots, i.e. window position j = f >> LD of residue rho0 + (f & (D-1))
+  auto plane = [&](int r, int s) {
+    const int64_t row = row0 + r;
+    const bool ok = row < rows;
+    const T* base = ok ? g + ((row * g_scales + st.chan[s]) * st.n_out) * C : g;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), (short)0,
+                                             ok ? (int)(st.n_out * C * (int64_t)sizeof(T)) : 0,
+                                             0x00020000);
+  };
+  T pf[MA_PFN][C];
+  auto prefetch = [&](int s) {
+    const int64_t qb = lo - st.x_off + rho0 + (int64_t)dil * (i0 - st.sup[s]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const __amdgpu_buffer_rsrc_t pr = plane(r, s);
+#pragma unroll
+      for (int m = 0; m < D; ++m) {
+        const int f = tid + NT * m;
+        const int64_t q = qb + (f & (D - 1)) + (int64_t)dil * (f >> LD);
+        ma_load<T, C>(pr, (int)(q * C * (int64_t)sizeof(T)), pf[r * D + m]);
+      }
+    }
+  };
+  const int i_l = lane & 15, kap = lane >> 4;
+  v4 acc[MA_NB];
+#pragma unroll
+  for (int b = 0; b < MA_NB; ++b) acc[b] = v4{T(0), T(0), T(0), T(0)};
+  if (st.n_scales > 0) prefetch(0);
+  for (int s = 0; s < st.n_scales; ++s) {
+    const int sup = st.sup[s];
+    const int wl = MA_TI + 2 * sup + 3;  // staged window positions
+    __syncthreads();  // the previous scale's reads of U and Fz are done
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+#pragma unroll
+      for (int m = 0; m < D; ++m) {
+        const int f = tid + NT * m, j = f >> LD;
+        if (j < wl) {
+          T* u = U + (r * D + (f & (D - 1))) * WS + j;
+#pragma unroll
+          for (int c = 0; c < C; ++c) u[c * 16 * WS] = pf[r * D + m][c];
+        }
+      }
+    }
+    {  // the scale's filters, zero-padded: Fz[c][z] = F_{s,c}[z - PADL]
+      const T* tp = taps + s * (half + 1) * C;
+      for (int e = tid; e < C * FL; e += NT) {
+        const int c = e / FL, k = e % FL - PADL, a = k < 0 ? -k : k;
+        T v = T(0);
+        if (a <= sup) {
+          v = tp[a * C + c];
+          if (c == 1) v = k > 0 ? v : (k < 0 ? -v : T(0));
+        }
+        Fz[e] = v;
+      }
+    }
+    __syncthreads();
+    if (s + 1 < st.n_scales) prefetch(s + 1);
+    const int steps = (16 + 2 * sup + 3) / 4;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const T* ua = U + (c * 16 + i_l) * WS + 16 * MA_NB * wave + kap;
+      const T* zb = Fz + c * FL + PADL + kap - i_l - sup;
+      for (int t = 0; t < steps; ++t) {
+        const T b = zb[4 * t];
+#pragma unroll
+        for (int bb = 0; bb < MA_NB; ++bb) acc[bb] = Mfma16<T>::mma(ua[16 * bb + 4 * t], b, acc[bb]);
+      }
+    }
+  }
+  // result element e of lane l: line Mfma16::row(l, e) = (row, residue), output i = l % 16
+#pragma unroll
+  for (int bb = 0; bb < MA_NB; ++bb) {
+    const int64_t i = i0 + 16 * (MA_NB * wave + bb) + i_l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int mline = Mfma16<T>::row(lane, e);
+      const int64_t r = row0 + (mline >> LD);
+      const int64_t p = lo + rho0 + (mline & (D - 1)) + (int64_t)dil * i;
+      if (p < hi && r < rows) {
+        T* o = gx + r * st.n_in + p;
+        *o = accumulate ? *o + acc[bb][e] : acc[bb][e];
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ half-band chain step
 // y[n] (+)= t0 x[n + b] + sum_{t odd <= c} taps[t] (x[n + b - dil t] + x[n + b + dil t])
 template <typename T>
@@ -1422,6 +1595,43 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
   if (n_out == 0) return FDWT_ERR_ARG;
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
+  {
+    // matrix-core kernel over the range g reaches (as the windowed kernel below), when its
+    // LDS (the staged window of 16 rows and the filter tables) fits and every g position a
+    // workgroup touches (-dil (half + MA_TI + 4) .. n_out + the same) is within the 2^31
+    // bytes of a plane's 32-bit buffer offsets
+    const int64_t reach = (int64_t)dil * half;
+    const int64_t lo = std::min(std::max(x_off - reach, (int64_t)0), n_in);
+    const int64_t hi = std::min(std::max(x_off + n_out + reach, lo), n_in);
+    const size_t lds = (size_t)channels * (16 * ma_ws(half) + ma_fl(half)) * cs;
+    const int64_t itiles = cdiv(std::max((int64_t)1, cdiv(hi - lo, dil)), MA_TI);
+    const int d = dil < 16 ? dil : 16;  // residues per workgroup line group
+    const int64_t rblocks = dil / d;
+    const int64_t blocks = cdiv(rows, 16 / d) * itiles * rblocks;
+    if ((dil & (dil - 1)) == 0 && MA_TI + 2 * half + 3 <= MA_WL && lds <= 64 * 1024 &&
+        itiles <= INT32_MAX &&
+        (n_out + 2 * (int64_t)dil * (half + MA_TI + 4)) * channels * cs < ((int64_t)1 << 31)) {
+#define ADM_D(TYPE, CPLX, DD)                                                                \
+  case DD: {                                                                                 \
+    auto k = morlet_adjoint_mfma_kernel<TYPE, CPLX, DD>;                                     \
+    FDWT_LDS_ONCE(k);                                                                        \
+    return launch(k, blocks, lds, hs, st, (const TYPE*)g, (TYPE*)gx, (int)g_scales, rows,     \
+                  (int)rblocks, (int)itiles, lo, hi, (int)accumulate);                       \
+  }
+#define ADM(TYPE, CPLX)                                                                      \
+  switch (d) {                                                                               \
+    ADM_D(TYPE, CPLX, 1) ADM_D(TYPE, CPLX, 2) ADM_D(TYPE, CPLX, 4) ADM_D(TYPE, CPLX, 8)      \
+    ADM_D(TYPE, CPLX, 16) default: break;                                                    \
+  }
+      if (dtype == FDWT_F32) {
+        if (channels == 2) ADM(float, true) else ADM(float, false)
+      } else {
+        if (channels == 2) ADM(double, true) else ADM(double, false)
+      }
+#undef ADM
+#undef ADM_D
+    }
+  }
   if ((dil & (dil - 1)) == 0 &&
       (n_out + 2 * (int64_t)dil * (half + RUN + 1)) * channels * cs < ((int64_t)1 << 31)) {
     // windowed kernel (power-of-two dilation, and g positions -2 dil H .. n_out + 2 dil H of
