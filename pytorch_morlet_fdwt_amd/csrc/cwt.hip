@@ -1504,7 +1504,7 @@ inline int resident_blocks(K kernel, size_t lds, int64_t cap) {
 template <typename K, typename... Args>
 int launch(K kernel, int64_t blocks, size_t lds, hipStream_t st, Args... args) {
   if (blocks <= 0) return 0;
-  if (blocks > INT32_MAX) return FDWT_ERR_ARG;
+  if (blocks > (int64_t)(0xffffffffu / NT)) return FDWT_ERR_ARG;  // 2^32 - 1 threads per launch
   if (lds > 160 * 1024) return FDWT_ERR_TOO_LONG;
   hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(NT), lds, st, args...);
   FDWT_CHECK_LAUNCH();

@@ -1774,8 +1774,20 @@ extern "C" int fdwt_analysis_chain(const void* x, void* const* details, void* ap
     a.split = (int)std::max<int64_t>(1, cdiv(nchunks, want));
     wg = (int)cdiv(nchunks, a.split);
   }
-  if (rows * wg > INT32_MAX) return FDWT_ERR_ARG;
-  return dispatch_achain(a, rows, wg, lds, nt, dtype, static_cast<hipStream_t>(stream));
+  // a launch holds at most 2^32 - 1 threads: larger batches run as consecutive launches over
+  // row ranges (the row pointers offset accordingly)
+  const int64_t per = std::max<int64_t>(1, (int64_t)(0xffffffffu / (unsigned)nt) / wg);
+  const int es = dtype_size(dtype);
+  for (int64_t r0 = 0; r0 < rows; r0 += per) {
+    AChainArgs c = a;
+    c.x = static_cast<const char*>(a.x) + r0 * n_in[0] * es;
+    for (int l = 0; l < levels; ++l) c.details[l] = static_cast<char*>(a.details[l]) + r0 * n_out[l] * es;
+    c.approx = static_cast<char*>(a.approx) + r0 * n_out[levels - 1] * es;
+    const int rc = dispatch_achain(c, std::min(per, rows - r0), wg, lds, nt, dtype,
+                                   static_cast<hipStream_t>(stream));
+    if (rc) return rc;
+  }
+  return 0;
 }
 
 // Whole-row synthesis chain: LDS layout, level records and prefetch jobs, launch.
@@ -1908,44 +1920,9 @@ extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* detai
     wg = (int)cdiv(m, per);
   }
   if (!a.split) return synthesis_rows(a, rows, dtype, static_cast<hipStream_t>(stream));
-  // per-level pass geometry of whole-row workgroups, and the queue of small-level high bands
+  // split mode (one level, long rows): no queued high bands
   a.qslots = 0;
   a.qlevels = 0;
-  if (!a.split) {
-    int slot = 0;
-    bool fits = true;
-    for (int l = 0; l < levels; ++l) {
-      const int md = normalize_mode(mode, (int)n_out[l]);
-      const int64_t pmin = off - (taps - 1);
-      const int64_t pmax = 2 * (nc[l] - 1) + off;
-      const int64_t nx = md == FDWT_MODE_ZERO ? 0
-                         : std::max<int64_t>(0, -pmin) + std::max<int64_t>(0, pmax - n_out[l] + 1);
-      const int64_t pbeg = nx > 0 ? std::min<int64_t>(0, pmin) : 0;
-      const int64_t pend = nx > 0 ? std::max<int64_t>(n_out[l], pmax + 1) : n_out[l];
-      const int64_t ub0 = ((pbeg + 1 - off) >> 1) & ~(int64_t)(VS - 1);
-      a.ub0[l] = (int32_t)ub0;
-      // the queue takes a prefix of the levels (never the last), each a single pass
-      if (fits && l + 1 < levels) {
-        const int64_t ub_last = (pend - off) >> 1;
-        const int64_t len = ub_last - ub0 + 2 * VS + taps / 2 + 4;
-        const int ns = (int)cdiv(len, NT);
-        if (ub_last - ub0 + 1 > PS || slot + ns > QR) {
-          fits = false;
-        } else {
-          a.qs0[l] = slot;
-          a.qsn[l] = ns;
-          a.qlen[l] = (int32_t)len;
-          for (int k = 0; k < ns; ++k, ++slot) {
-            a.qs_ptr[slot] = a.details[l];
-            a.qs_nc[slot] = (int32_t)nc[l];
-            a.qs_u0[slot] = (int32_t)(ub0 + (int64_t)k * NT);
-          }
-          a.qlevels = l + 1;
-        }
-      }
-    }
-    a.qslots = slot;
-  }
   int capA, capB, capE, capD;
   schain_caps(nc, n_out, levels, taps, off, mode, a.split, &capA, &capB, &capE, &capD);
   a.capA = capA;
@@ -1958,8 +1935,20 @@ extern "C" int fdwt_synthesis_chain(const void* approx, const void* const* detai
                      (size_t)(capA + capB + capE + (2 * capE + 8) + capD + 2 * taps + 4) * cs +
                      (size_t)capE * 4;
   if (!fits_lds((int64_t)lds)) return FDWT_ERR_TOO_LONG;
-  if (rows * wg > INT32_MAX) return FDWT_ERR_ARG;
-  return dispatch_schain(a, rows, wg, lds, dtype, static_cast<hipStream_t>(stream));
+  // at most 2^32 - 1 threads per launch: consecutive launches over row ranges
+  const int64_t per = std::max<int64_t>(1, (int64_t)(0xffffffffu / (unsigned)NT) / wg);
+  const int es = dtype_size(dtype);
+  for (int64_t r0 = 0; r0 < rows; r0 += per) {
+    SChainArgs c = a;
+    if (a.approx) c.approx = static_cast<const char*>(a.approx) + r0 * nc[0] * es;
+    for (int l = 0; l < levels; ++l)
+      if (a.details[l]) c.details[l] = static_cast<const char*>(a.details[l]) + r0 * nc[l] * es;
+    c.out = static_cast<char*>(a.out) + r0 * n_out[levels - 1] * es;
+    const int rc = dispatch_schain(c, std::min(per, rows - r0), wg, lds, dtype,
+                                   static_cast<hipStream_t>(stream));
+    if (rc) return rc;
+  }
+  return 0;
 }
 
 extern "C" int fdwt_dwt_analysis(const void* x, void* y0, void* y1, const void* h0,

@@ -140,6 +140,26 @@ def test_fused_backward_matches_oracle(mode):
         torch.testing.assert_close(xg.grad.cpu(), xc.grad, atol=1e-11, rtol=1e-11)
 
 
+def test_analysis_rows_past_one_launch():
+    """A launch holds at most 2^32 - 1 threads: the 128-thread analysis chain takes 33,554,431
+    rows per launch, so 33,554,433 rows of 2 samples run as two launches over row ranges.
+    Rows at the start and end (the second launch) match the oracle; every row matches the
+    Haar closed form of its two samples."""
+    R = 33_554_433
+    x = torch.randn(R, 2, generator=torch.Generator().manual_seed(3))
+    xd = x.to(DEV)
+    ca, cd = fdwt.wavedec(xd, "haar", "periodization", 1)
+    torch.cuda.synchronize()
+    for sl in (slice(0, 4), slice(R - 4, R)):
+        ra, rd = O.wavedec(x[sl].double(), "haar", "periodization", 1)
+        torch.testing.assert_close(ca[sl].cpu().double(), ra, atol=1e-6, rtol=1e-6)
+        torch.testing.assert_close(cd[sl].cpu().double(), rd, atol=1e-6, rtol=1e-6)
+    s = 2 ** -0.5
+    torch.testing.assert_close(ca[:, 0], (xd[:, 0] + xd[:, 1]) * s, atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(cd[:, 0].abs(), (xd[:, 0] - xd[:, 1]).abs() * s, atol=1e-6,
+                               rtol=1e-6)
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_chains_deeper_than_one_launch(mode):
     """More levels than one synthesis launch takes (FDWT_SYN_MAX_LEVELS = 16): lengths
