@@ -20,6 +20,7 @@ _LOCK = threading.Lock()
 _LIB = None
 
 DTYPE = {torch.float32: 0, torch.float64: 1, torch.float16: 2, torch.bfloat16: 3}
+F32_BF16 = 4  # fp32 storage, bf16 matrix-core operands (FDWT_F32_BF16)
 ERR_TOO_LONG = -2
 ERR_SCRATCH = -3
 

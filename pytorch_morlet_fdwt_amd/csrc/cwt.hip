@@ -864,9 +864,28 @@ constexpr int MA_TI = 4 * 16 * MA_NB;  // outputs per line of a workgroup
 constexpr int MA_WL = 256;             // longest staged window (half <= (MA_WL - MA_TI - 3) / 2)
 constexpr int MA_PFN = 16 * MA_WL / NT;  // prefetch loads per thread (16 lines x MA_WL)
 
-// LDS line stride (elements) of the staged u and length of a filter table, for a stage's half
-__host__ __device__ inline int ma_ws(int half) { return 32 * ((MA_TI + 2 * half - 1 + 31) / 32) + 4; }
-__host__ __device__ inline int ma_fl(int half) { return 2 * half + 34; }
+// bf16 operands (fp32 storage and accumulation): one v_mfma_f32_16x16x16_bf16 per 16 window
+// positions, so the window is staged 12 positions longer (MA_TI + 2 sup + 15), in bf16.
+// LDS line stride (elements) of the staged u, length of an fp32 filter table, and (bf16) the
+// steps of the B-operand table, for a stage's half
+__host__ __device__ inline int ma_ext(bool bf) { return bf ? 15 : 3; }
+__host__ __device__ inline int ma_ws(int half, bool bf = false) {
+  return 32 * ((MA_TI + 2 * half + ma_ext(bf) - 4 + 31) / 32) + 4;
+}
+__host__ __device__ inline int ma_fl(int half, bool bf = false) { return 2 * half + (bf ? 48 : 34); }
+// LDS bytes of the matrix-core adjoint: the staged window and the zero-padded filter table,
+// both in the operand type
+__host__ __device__ inline int64_t ma_lds(int half, int C, int es, bool bf) {
+  return (int64_t)C * (16 * ma_ws(half, bf) + ma_fl(half, bf)) * (bf ? 2 : es);
+}
+
+// float -> bf16 bits, round to nearest even (NaN stays a NaN)
+__device__ inline uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
 
 // One g position (C values, re then im) through a buffer resource; 0 outside its range.
 template <typename T, int C>
@@ -883,7 +902,7 @@ __device__ inline void ma_load(__amdgpu_buffer_rsrc_t r, int off, T (&v)[C]) {
   }
 }
 
-template <typename T, bool CPLX, int D>
+template <typename T, bool CPLX, int D, bool BF>  // BF: bf16 operands (T = float)
 __global__ void __launch_bounds__(NT) morlet_adjoint_mfma_kernel(Stage st, const T* __restrict__ g,
                                                                  T* __restrict__ gx, int g_scales,
                                                                  int64_t rows, int rblocks,
@@ -893,12 +912,15 @@ __global__ void __launch_bounds__(NT) morlet_adjoint_mfma_kernel(Stage st, const
   constexpr int RW = 16 / D;            // rows of a workgroup
   constexpr int LD = __builtin_ctz(D);
   static_assert(MA_PFN % D == 0 && MA_PFN / D == RW, "D * MA_WL slots per row");
+  static_assert(!BF || std::is_same<T, float>::value, "bf16 operands with float storage");
   typedef typename Mfma16<T>::v4 v4;
+  typedef typename std::conditional<BF, uint16_t, T>::type E;  // staged window element
+  typedef short v4s __attribute__((ext_vector_type(4)));
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int half = st.half, dil = st.dil;
-  const int WS = ma_ws(half), FL = ma_fl(half), PADL = half + 15;
-  T* const U = reinterpret_cast<T*>(smem_raw);  // [C][16][WS]
-  T* const Fz = U + C * 16 * WS;                // [C][FL]
+  const int WS = ma_ws(half, BF), FL = ma_fl(half, BF), PADL = half + 15;
+  E* const U = reinterpret_cast<E*>(smem_raw);  // [C][16][WS]
+  E* const Fz = U + C * 16 * WS;                // [C][FL]: F_{s,c}[z - PADL], 0 elsewhere
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t blk = blockIdx.x;
   const int rb = (int)(blk % rblocks);
@@ -949,43 +971,68 @@ __global__ void __launch_bounds__(NT) morlet_adjoint_mfma_kernel(Stage st, const
   if (st.n_scales > 0) prefetch(0);
   for (int s = 0; s < st.n_scales; ++s) {
     const int sup = st.sup[s];
-    const int wl = MA_TI + 2 * sup + 3;  // staged window positions
-    __syncthreads();  // the previous scale's reads of U and Fz are done
+    const int wl = MA_TI + 2 * sup + ma_ext(BF);  // staged window positions
+    const T* tp = taps + s * (half + 1) * C;
+    // F_{s,c}[k], |k| <= sup, from the compact taps (0 beyond the support)
+    auto filt = [&](int c, int k) {
+      const int a = k < 0 ? -k : k;
+      T v = T(0);
+      if (a <= sup) {
+        v = tp[a * C + c];
+        if (c == 1) v = k > 0 ? v : (k < 0 ? -v : T(0));
+      }
+      return v;
+    };
+    __syncthreads();  // the previous scale's reads of U and the filter table are done
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
 #pragma unroll
       for (int m = 0; m < D; ++m) {
         const int f = tid + NT * m, j = f >> LD;
         if (j < wl) {
-          T* u = U + (r * D + (f & (D - 1))) * WS + j;
+          E* u = U + (r * D + (f & (D - 1))) * WS + j;
 #pragma unroll
-          for (int c = 0; c < C; ++c) u[c * 16 * WS] = pf[r * D + m][c];
+          for (int c = 0; c < C; ++c) {
+            if constexpr (BF) u[c * 16 * WS] = f2bf(pf[r * D + m][c]);
+            else u[c * 16 * WS] = pf[r * D + m][c];
+          }
         }
       }
     }
-    {  // the scale's filters, zero-padded: Fz[c][z] = F_{s,c}[z - PADL]
-      const T* tp = taps + s * (half + 1) * C;
-      for (int e = tid; e < C * FL; e += NT) {
-        const int c = e / FL, k = e % FL - PADL, a = k < 0 ? -k : k;
-        T v = T(0);
-        if (a <= sup) {
-          v = tp[a * C + c];
-          if (c == 1) v = k > 0 ? v : (k < 0 ? -v : T(0));
-        }
-        Fz[e] = v;
-      }
+    const int steps = BF ? (16 + 2 * sup + 15) / 16 : (16 + 2 * sup + 3) / 4;
+    for (int e = tid; e < C * FL; e += NT) {
+      const T v = filt(e / FL, e % FL - PADL);
+      if constexpr (BF) Fz[e] = f2bf(v);
+      else Fz[e] = v;
     }
     __syncthreads();
     if (s + 1 < st.n_scales) prefetch(s + 1);
-    const int steps = (16 + 2 * sup + 3) / 4;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const T* ua = U + (c * 16 + i_l) * WS + 16 * MA_NB * wave + kap;
-      const T* zb = Fz + c * FL + PADL + kap - i_l - sup;
-      for (int t = 0; t < steps; ++t) {
-        const T b = zb[4 * t];
+      if constexpr (BF) {
+        // A: U[l % 16][16 tb + 16 t + 4 (l / 16) + v], v < 4 (8-byte aligned: WS % 4 == 0);
+        // B: Z[16 t + 4 (l / 16) + v][l % 16] = F[16 t + 4 (l / 16) + v - l % 16 - sup]
+        const E* ua = U + (c * 16 + i_l) * WS + 16 * MA_NB * wave + 4 * kap;
+        const E* zb = Fz + c * FL + PADL + 4 * kap - i_l - sup;
+        for (int t = 0; t < steps; ++t) {
+          v4s b;
 #pragma unroll
-        for (int bb = 0; bb < MA_NB; ++bb) acc[bb] = Mfma16<T>::mma(ua[16 * bb + 4 * t], b, acc[bb]);
+          for (int v = 0; v < 4; ++v) b[v] = (short)zb[16 * t + v];
+#pragma unroll
+          for (int bb = 0; bb < MA_NB; ++bb) {
+            const v4s a = *reinterpret_cast<const v4s*>(ua + 16 * bb + 16 * t);
+            acc[bb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc[bb], 0, 0, 0);
+          }
+        }
+      } else {
+        const E* ua = U + (c * 16 + i_l) * WS + 16 * MA_NB * wave + kap;
+        const T* zb = Fz + c * FL + PADL + kap - i_l - sup;
+        for (int t = 0; t < steps; ++t) {
+          const T b = zb[4 * t];
+#pragma unroll
+          for (int bb = 0; bb < MA_NB; ++bb)
+            acc[bb] = Mfma16<T>::mma(ua[16 * bb + 4 * t], b, acc[bb]);
+        }
       }
     }
   }
@@ -1587,7 +1634,8 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
   // the stage's x is unused here; pass g to satisfy the null check
   int e = fill_stage(st, g, taps, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
   if (e) return e;
-  if (!gx || rows < 0 || g_scales < 1 || (dtype != FDWT_F32 && dtype != FDWT_F64))
+  if (!gx || rows < 0 || g_scales < 1 ||
+      (dtype != FDWT_F32 && dtype != FDWT_F64 && dtype != FDWT_F32_BF16))
     return FDWT_ERR_ARG;
   for (int s = 0; s < n_scales; ++s)
     if (chan[s] >= g_scales) return FDWT_ERR_ARG;
@@ -1603,34 +1651,38 @@ extern "C" int fdwt_morlet_backward_x(const void* g, const void* taps, void* gx,
     const int64_t reach = (int64_t)dil * half;
     const int64_t lo = std::min(std::max(x_off - reach, (int64_t)0), n_in);
     const int64_t hi = std::min(std::max(x_off + n_out + reach, lo), n_in);
-    const size_t lds = (size_t)channels * (16 * ma_ws(half) + ma_fl(half)) * cs;
+    const bool bf = dtype == FDWT_F32_BF16;
+    const size_t lds = (size_t)ma_lds(half, channels, cs, bf);
     const int64_t itiles = cdiv(std::max((int64_t)1, cdiv(hi - lo, dil)), MA_TI);
     const int d = dil < 16 ? dil : 16;  // residues per workgroup line group
     const int64_t rblocks = dil / d;
     const int64_t blocks = cdiv(rows, 16 / d) * itiles * rblocks;
-    if ((dil & (dil - 1)) == 0 && MA_TI + 2 * half + 3 <= MA_WL && lds <= 64 * 1024 &&
+    if ((dil & (dil - 1)) == 0 && MA_TI + 2 * half + ma_ext(bf) <= MA_WL && lds <= 64 * 1024 &&
         itiles <= INT32_MAX &&
-        (n_out + 2 * (int64_t)dil * (half + MA_TI + 4)) * channels * cs < ((int64_t)1 << 31)) {
-#define ADM_D(TYPE, CPLX, DD)                                                                \
+        (n_out + 2 * (int64_t)dil * (half + MA_TI + 16)) * channels * cs < ((int64_t)1 << 31)) {
+#define ADM_D(TYPE, CPLX, DD, BF)                                                            \
   case DD: {                                                                                 \
-    auto k = morlet_adjoint_mfma_kernel<TYPE, CPLX, DD>;                                     \
+    auto k = morlet_adjoint_mfma_kernel<TYPE, CPLX, DD, BF>;                                 \
     FDWT_LDS_ONCE(k);                                                                        \
     return launch(k, blocks, lds, hs, st, (const TYPE*)g, (TYPE*)gx, (int)g_scales, rows,     \
                   (int)rblocks, (int)itiles, lo, hi, (int)accumulate);                       \
   }
-#define ADM(TYPE, CPLX)                                                                      \
+#define ADM(TYPE, CPLX, BF)                                                                  \
   switch (d) {                                                                               \
-    ADM_D(TYPE, CPLX, 1) ADM_D(TYPE, CPLX, 2) ADM_D(TYPE, CPLX, 4) ADM_D(TYPE, CPLX, 8)      \
-    ADM_D(TYPE, CPLX, 16) default: break;                                                    \
+    ADM_D(TYPE, CPLX, 1, BF) ADM_D(TYPE, CPLX, 2, BF) ADM_D(TYPE, CPLX, 4, BF)               \
+    ADM_D(TYPE, CPLX, 8, BF) ADM_D(TYPE, CPLX, 16, BF) default: break;                       \
   }
-      if (dtype == FDWT_F32) {
-        if (channels == 2) ADM(float, true) else ADM(float, false)
+      if (bf) {
+        if (channels == 2) ADM(float, true, true) else ADM(float, false, true)
+      } else if (dtype == FDWT_F32) {
+        if (channels == 2) ADM(float, true, false) else ADM(float, false, false)
       } else {
-        if (channels == 2) ADM(double, true) else ADM(double, false)
+        if (channels == 2) ADM(double, true, false) else ADM(double, false, false)
       }
 #undef ADM
 #undef ADM_D
     }
+    if (bf) dtype = FDWT_F32;  // bf16 operands are a permission: the other kernels stay fp32
   }
   if ((dil & (dil - 1)) == 0 &&
       (n_out + 2 * (int64_t)dil * (half + RUN + 1)) * channels * cs < ((int64_t)1 << 31)) {
@@ -1721,6 +1773,7 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
   Stage st;
   int e = fill_stage(st, x, g, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
   if (e) return e;
+  if (dtype == FDWT_F32_BF16) dtype = FDWT_F32;  // no bf16 kernel here: fp32 operands
   if (!workspace || !gh || rows < 0 || (dtype != FDWT_F32 && dtype != FDWT_F64)) return FDWT_ERR_ARG;
   for (int s = 0; s < n_scales; ++s)
     if (chan[s] >= g_scales) return FDWT_ERR_ARG;
@@ -1868,7 +1921,7 @@ extern "C" int fdwt_morlet_backward_h_noalloc(const void* x, const void* g, void
                                               const int32_t* support, const int32_t* chan,
                                               int32_t dil, int32_t channels, int32_t g_scales,
                                               int32_t accumulate, int32_t dtype, void* stream) {
-  if (dtype != FDWT_F32 && dtype != FDWT_F64) return FDWT_ERR_ARG;
+  if (dtype != FDWT_F32 && dtype != FDWT_F64 && dtype != FDWT_F32_BF16) return FDWT_ERR_ARG;
   void* ws = nullptr;
   const int e = noalloc_scratch(&ws);
   if (e) return e;

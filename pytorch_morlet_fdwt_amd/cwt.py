@@ -31,6 +31,7 @@ import torch
 from torch import nn
 
 from . import _lib
+from .config import resolve_precision
 
 __all__ = ["cwt", "CWT1D", "MorletPlan", "freqs_to_scales", "scales_to_freqs", "morlet_mix",
            "spectral_softmax"]
@@ -323,20 +324,30 @@ def _lowpass_chain(plan: MorletPlan, x: torch.Tensor) -> List[torch.Tensor]:
     return xs
 
 
+def _operand_code(dt, precision: str) -> int:
+    """C-ABI dtype code of the bank's backward entry points: fp32 storage with bf16 matrix
+    operands for the reference's "bf16" precision (conv.py:192-196), else the storage dtype.
+    ("tf32" computes in fp32: CDNA4 has no TF32 matrix format.)"""
+    if precision == "bf16" and dt == torch.float32:
+        return _lib.F32_BF16
+    return _lib.dtype_code(dt)
+
+
 def _stage_backward(plan, k, grp: _Group, xj, g, g_scales, chan, taps, gx, accumulate,
-                    need_h):
+                    need_h, precision: str = "ieee"):
     """grad-x of one launch group (accumulated into gx) and, if asked, the group's tap
     gradient (g1 - g0, 2 half + 1, C).  ``chan`` gives the group's channels in g, ``taps``
-    is the stage's whole tap table."""
+    is the stage's whole tap table; ``precision`` as ``resolve_precision`` returns it."""
     st = plan.stages[k]
     R, n_out = g.shape[0], g.shape[2]
     C = plan.channels
     mj = plan.margins[st.octave]
     dev, dt = g.device, g.dtype
     tg = taps[grp.g0:grp.g1]
+    code = _operand_code(dt, precision)
     _lib.launch("fdwt_morlet_backward_x", dev, _lib.ptr(g), _lib.ptr(tg), _lib.ptr(gx), R,
                 gx.shape[1], n_out, mj, grp.n, st.half, grp.sup, chan, st.dil, C,
-                g_scales, int(accumulate), _lib.dtype_code(dt), _lib.stream(dev))
+                g_scales, int(accumulate), code, _lib.stream(dev))
     if not need_h:
         return None
     L = _lib.lib()
@@ -345,7 +356,7 @@ def _stage_backward(plan, k, grp: _Group, xj, g, g_scales, chan, taps, gx, accum
     gh = torch.empty((grp.n, 2 * st.half + 1, C), device=dev, dtype=dt)
     _lib.launch("fdwt_morlet_backward_h", dev, _lib.ptr(xj), _lib.ptr(g), _lib.ptr(ws), ws_n,
                 _lib.ptr(gh), R, xj.shape[1], n_out, mj, grp.n, st.half, grp.sup, chan,
-                st.dil, C, g_scales, 0, _lib.dtype_code(dt), _lib.stream(dev))
+                st.dil, C, g_scales, 0, code, _lib.stream(dev))
     return gh
 
 
@@ -418,7 +429,8 @@ class _MorletCWTFunction(torch.autograd.Function):
                 ghs = []
                 for grp in _stage_groups(plan, k):
                     gh = _stage_backward(plan, k, grp, xs[j] if ctx.need_h else None, g,
-                                         plan.num_scales, grp.chan, taps, gx, filled, ctx.need_h)
+                                         plan.num_scales, grp.chan, taps, gx, filled, ctx.need_h,
+                                         resolve_precision(g.dtype))
                     filled = True
                     if gh is not None:
                         ghs.append(gh)
@@ -492,6 +504,7 @@ class _MorletMixFunction(torch.autograd.Function):
         xs = saved[:nx]
         H, a, b = saved[nx:nx + 3]
         gy = gy.contiguous().to(a.dtype)
+        prec = resolve_precision(gy.dtype)  # the compute dtype, as the reference's launchers
         R, N = gy.shape
         D = a.shape[0]
         C = plan.channels
@@ -538,7 +551,7 @@ class _MorletMixFunction(torch.autograd.Function):
                         ga[:, idx[grp.g0:grp.g1]] += part[..., 0]
                         gb[:, idx[grp.g0:grp.g1]] += part[..., 1]
                         gh = _stage_backward(plan, k, grp, xj, gw, S_g, grp.local, taps,
-                                             gx[r0:r1], filled, need_h)
+                                             gx[r0:r1], filled, need_h, prec)
                         if gh is not None:
                             gh_acc = gh if gh_acc is None else gh_acc + gh
                         del gw
@@ -611,7 +624,7 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
                     first = False
             if j + 1 < plan.n_octaves and j < last_j:
                 xj = _lowpass_step(plan, xj, j, N)
-        ctx.plan, ctx.nch, ctx.tau = plan, nch, tau
+        ctx.plan, ctx.nch, ctx.tau, ctx.precision = plan, nch, tau, precision
         ctx.x_dtype, ctx.v_dtype = x.dtype, V.dtype
         ctx.tables = tables
         ctx.save_for_backward(x, H, V_, m, l, out)
@@ -622,6 +635,7 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
         plan: MorletPlan = ctx.plan
         x, H, V, m, l, out = ctx.saved_tensors
         gy = gy.contiguous().to(V.dtype)
+        prec = ctx.precision
         R, N = gy.shape
         dev, dt = gy.device, gy.dtype
         v_pos = V.dim() == 3
@@ -673,7 +687,7 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
                             part = ws[:ws_n].view(rc, -1, S_g).sum(1).view(-1, nch, S_g).sum(0)
                             gV[:, gidx] += part
                         gh = _stage_backward(plan, k, grp, xj, gw, S_g, grp.local, taps,
-                                             gx[r0:r1], filled, need_h)
+                                             gx[r0:r1], filled, need_h, prec)
                         if gh is not None:
                             gh_acc = gh if gh_acc is None else gh_acc + gh
                         del gw
@@ -699,10 +713,10 @@ def spectral_softmax(x: torch.Tensor, plan: MorletPlan, H: torch.Tensor, V: torc
     _lib.require_gpu(x)
     if R % nch:
         raise ValueError(f"the number of rows {R} must be a multiple of nch={nch}")
+    prec = resolve_precision(x.dtype)  # the caller's dtype: bf16 / fp16 inputs select bf16
     x2 = x.contiguous()
     if x2.dtype not in (torch.float32, torch.float64):
         x2 = x2.float()
-    prec = "ieee"
     return _SpectralSoftmaxFunction.apply(x2, plan, H, V, nch, float(tau), prec)
 
 

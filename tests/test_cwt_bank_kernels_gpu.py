@@ -119,3 +119,47 @@ def _tap_gradient(x, g, half, dil, x_off, n_out):
     H = torch.zeros(S, 2 * half + 1, C, dtype=x.dtype, requires_grad=True)
     (gH,) = torch.autograd.grad(_forward(x, H, half, dil, x_off, n_out), [H], g)
     return gH
+
+
+# stages the bf16 matrix-core adjoint takes (power-of-two dilation, at most 56 taps per side);
+# the others compute in fp32 (bf16 operands are a permission, not a requirement)
+BF16_CASES = [c for c in CASES if c[1] <= 56 and c[0] & (c[0] - 1) == 0]
+
+
+@pytest.mark.parametrize("case", BF16_CASES, ids=[f"d{c[0]}h{c[1]}C{c[3]}m{c[4]}a{c[5]}" for c in BF16_CASES])
+def test_bank_adjoint_bf16_operands(case):
+    """FDWT_F32_BF16 (the reference's "bf16" precision, conv.py:192-196): g and the taps are
+    rounded to bf16, products and sums are fp32.  Against the adjoint of the bf16-rounded
+    operands computed in float64 the kernel must agree to fp32 accumulation (1e-5 of the
+    largest value); against the exact adjoint to the reference's ~5e-3 (README.md:206-212)."""
+    dil, half, sup, C, margin, acc = case
+    R, n_out, S, g_scales = 3, 700, len(sup), len(sup) + 2
+    chan = [(2 * s + 1) % g_scales for s in range(S)]
+    n_in, x_off = n_out + 2 * margin, margin
+    gen = torch.Generator().manual_seed(dil * 1000 + half + 7)
+    f64 = torch.float64
+    taps = torch.randn(S, half + 1, C, dtype=f64, generator=gen).float()
+    g = torch.randn(R, g_scales, n_out, C, dtype=f64, generator=gen).float()
+    gx0 = torch.randn(R, n_in, dtype=f64, generator=gen).float()
+
+    def adjoint(t, gg):
+        x = torch.zeros(R, n_in, dtype=f64, requires_grad=True)
+        (gx,) = torch.autograd.grad(_forward(x, _full_taps(t.double(), sup), half, dil, x_off,
+                                             n_out), [x], gg[:, chan].double())
+        return gx + gx0.double() if acc else gx
+
+    bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    ref_bf = adjoint(bf(taps), bf(g))
+    ref = adjoint(taps, g)
+    gd, td = g.to(DEV).contiguous(), taps.to(DEV).contiguous()
+    gx = gx0.to(DEV).contiguous() if acc else torch.full((R, n_in), float("nan"), device=DEV)
+    _lib.launch("fdwt_morlet_backward_x", torch.device(DEV), _lib.ptr(gd), _lib.ptr(td),
+                _lib.ptr(gx), R, n_in, n_out, x_off, S, half, _i32(sup), _i32(chan), dil, C,
+                g_scales, acc, _lib.F32_BF16, _lib.stream(torch.device(DEV)))
+    torch.cuda.synchronize()
+    got = gx.cpu().double()
+    assert torch.isfinite(got).all()
+    scale = ref_bf.abs().max().item()
+    torch.testing.assert_close(got, ref_bf, rtol=0, atol=1e-5 * scale)
+    err = (got - ref).abs().max().item() / ref.abs().max().item()
+    assert err < 1e-2, err

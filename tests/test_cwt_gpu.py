@@ -269,6 +269,69 @@ def test_attention_fp32_and_bf16_run():
     np.testing.assert_allclose(m.freqs.cpu().numpy(), [2.0, 6.0, 12.0, 25.0], rtol=1e-5)
 
 
+def test_bf16_precision_mode_backward(monkeypatch):
+    """config.allow_bf16 (the reference's "bf16" precision: bf16 matrix operands, fp32
+    accumulation, README.md:206-212) rounds the bank adjoint's operands -- the upstream
+    scalogram gradient and the filters -- to bf16.  CWT: the input gradient matches the
+    float64 oracle gradient with exactly those operands rounded to bf16 (a CPU emulation of the
+    mode) to 2e-3 relative L2 error, while both miss the exact gradient by ~1.6e-2 (the mode's
+    own error on this problem: oscillatory filters against a wideband gradient cancel).
+    MorletAttention: forward outputs and parameter gradients unchanged (those kernels compute
+    in fp32), the input gradient within 8e-2 relative L2 error of float64 (4.6e-2 measured),
+    and bf16 inputs, which select the mode (cwt.py:540), within 1e-1 (6.1e-2 measured)."""
+    def rel(a, b):
+        return ((a - b).norm() / b.norm()).item()
+
+    freqs = torch.logspace(-0.3, 2, 40).tolist()
+    sig = torch.randn(4, 2500, generator=torch.Generator().manual_seed(8), dtype=torch.float64)
+    scales = O.freqs_to_scales(freqs, 250.0, 6.0).tolist()
+    plan = O.Plan(scales)
+    H = plan.filters(torch.tensor(scales, dtype=torch.float64), torch.tensor(6.0, dtype=torch.float64))
+
+    def oracle_grad(Hf, round_g):
+        xs = sig.clone().requires_grad_()
+        yr = torch.view_as_real(O.apply_plan(xs, plan, Hf))
+        wt = torch.cos(torch.arange(yr.numel(), dtype=torch.float64)).view_as(yr)
+        if round_g:
+            wt = wt.to(torch.bfloat16).double()
+        (g,) = torch.autograd.grad((yr * wt).sum(), [xs])
+        return g
+
+    exact = oracle_grad(H, False)
+    emulated = oracle_grad(H.to(torch.bfloat16).double(), True)
+    monkeypatch.setattr(fdwt.config, "allow_bf16", True)
+    xs = sig.float().to(DEV).requires_grad_()
+    yc = torch.view_as_real(fdwt.cwt(xs, freqs=freqs, fs=250, method="fast"))
+    wt = torch.cos(torch.arange(yc.numel(), device=DEV, dtype=torch.float64)).view_as(yc)
+    (g,) = torch.autograd.grad((yc.double() * wt).sum(), [xs])
+    g = g.double().cpu()
+    assert rel(g, emulated) < 2e-3, rel(g, emulated)
+    assert rel(g, exact) < 2.5e-2, rel(g, exact)
+    assert rel(emulated, exact) > 5e-3  # the mode's own error: the comparison above has teeth
+
+    torch.manual_seed(5)
+    m = fdwt.MorletAttention(num_channels=6, hidden_dim=200).to(DEV)
+    x = torch.randn(2, 2, 6, 10, 200, device=DEV)
+    w = torch.cos(torch.arange(x.numel(), device=DEV, dtype=torch.float64).view_as(x))
+
+    def run(dt, bf):
+        monkeypatch.setattr(fdwt.config, "allow_bf16", bf)
+        mm = m.to(torch.float64 if dt == torch.float64 else torch.float32)
+        mm.zero_grad()
+        xx = x.detach().to(dt).requires_grad_()
+        y = mm(xx)
+        (y.double() * w).sum().backward()
+        return [t.detach().double() for t in (y, xx.grad, mm.freq_weight.grad,
+                                               mm.cwt.log_scales.grad)]
+
+    r64, r32, rb, rbf = (run(torch.float64, False), run(torch.float32, False),
+                         run(torch.float32, True), run(torch.bfloat16, False))
+    assert torch.equal(rb[0], r32[0]) and torch.equal(rb[2], r32[2]) and torch.equal(rb[3], r32[3])
+    assert 1e-6 < rel(rb[1], r64[1]) < 8e-2, rel(rb[1], r64[1])
+    assert torch.isfinite(rbf[1]).all()
+    assert rel(rbf[1], r64[1]) < 1e-1, rel(rbf[1], r64[1])
+
+
 def test_fp32_attention_matches_fp64():
     """north-star fp32 bar on a cfg5-shaped problem: MorletAttention forward + backward."""
     torch.manual_seed(2)
