@@ -99,6 +99,29 @@ def lib():
     return _LIB
 
 
+_EXT = None
+_EXT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_fdwt_autograd.so")
+
+
+def ext():
+    """The C++ autograd nodes of the DWT chains (csrc/autograd.cpp), wired to this library's
+    entry points on first use; None when the extension is not built or a launch timer is
+    installed (the timer brackets Python-level launches only)."""
+    global _EXT
+    if _TIMER is not None or not os.path.exists(_EXT_PATH):
+        return None
+    if _EXT is None:
+        with _LOCK:
+            if _EXT is None:
+                L = lib()
+                from . import _fdwt_autograd as m
+                addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
+                m.set_entry_points(addr(L.fdwt_analysis_chain), addr(L.fdwt_synthesis_chain),
+                                   addr(L.fdwt_error_string))
+                _EXT = m
+    return _EXT
+
+
 class KernelTimer:
     """Optional per-entry-point timing: when installed (``set_timer``), every launch made
     through :func:`launch` is bracketed by HIP events on the stream it is enqueued on.

@@ -64,7 +64,31 @@ def build(jobs=None):
     return OUT
 
 
+EXT = os.path.join(PKG, "_fdwt_autograd.so")
+
+
+def build_ext():
+    """The C++ autograd nodes of the DWT chains (autograd.cpp), a torch extension built with
+    torch.utils.cpp_extension (g++, torch and ROCm headers) into ``_build/ext`` and copied into
+    the package as ``_fdwt_autograd.so``."""
+    import torch
+    from torch.utils import cpp_extension
+    bdir = os.path.join(HERE, "_build", "ext")
+    os.makedirs(bdir, exist_ok=True)
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    cpp_extension.load(
+        name="_fdwt_autograd", sources=[os.path.join(HERE, "autograd.cpp")],
+        extra_include_paths=["/opt/rocm/include"],
+        extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1"],
+        extra_ldflags=[f"-L{torch_lib}", "-lc10_hip"], build_directory=bdir, with_cuda=False,
+        verbose=False, is_python_module=True)
+    shutil.copyfile(os.path.join(bdir, "_fdwt_autograd.so"), EXT + ".tmp")
+    os.replace(EXT + ".tmp", EXT)
+    return EXT
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
     print(build(ap.parse_args().j))
+    print(build_ext())

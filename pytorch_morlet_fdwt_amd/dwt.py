@@ -85,6 +85,15 @@ def _chain_fits(n: int, taps: int, dtype) -> bool:
     return n <= _chain_max(taps, dtype)
 
 
+def _one_launch(levels: int, n: int, taps: int, dtype):
+    """The C++ autograd nodes when a chain of ``levels`` over rows of ``n`` samples and its
+    transpose both run as one launch (the common case), else None (dwt.py's Functions, which
+    split long rows and deep chains into several launches)."""
+    if levels > _SYN_MAX_LEVELS or (levels > 1 and not _chain_fits(n, taps, dtype)):
+        return None
+    return _lib.ext()
+
+
 def _analysis_chain(x2, h0, h1, mode, off, n_in, n_out, lead=None):
     """Levels l = 0..J-1 of an analysis chain on the contiguous rows of x2 (any shape
     (*lead, n_in[0])).  Returns (details, approx), shaped (*lead, n) when the whole chain is one
@@ -371,7 +380,12 @@ def wavedec(x: torch.Tensor, wavelet: WaveletLike = "db4", mode: str = "symmetri
         n_in.append(n)
         n = dwt_coeff_len(n, L, mode)
         n_out.append(n)
-    outs = _AnalysisChain.apply(x, f["dec_lo"], f["dec_hi"], m, off, tuple(n_in), tuple(n_out))
+    fast = _one_launch(level, x.shape[-1], L, x.dtype)
+    if fast is not None:
+        outs = fast.analysis_chain(x, f["dec_lo"], f["dec_hi"], m, off, n_in, n_out)
+    else:
+        outs = _AnalysisChain.apply(x, f["dec_lo"], f["dec_hi"], m, off, tuple(n_in),
+                                    tuple(n_out))
     return [outs[-1]] + list(outs[:-1])[::-1]
 
 
@@ -409,6 +423,9 @@ def waverec(coeffs: Sequence[torch.Tensor], wavelet: WaveletLike = "db4",
     if a is not None and a.shape[-1] == nc[0] + 1:
         a = a[..., :-1]
     ds = [d.to(ref.dtype) if d is not None else None for d in coeffs[1:]]
+    fast = _one_launch(len(nc), n_out[-1], L, ref.dtype)
+    if fast is not None:
+        return fast.synthesis_chain(f["rec_lo_rev"], f["rec_hi_rev"], mm, off, nc, n_out, a, ds)
     return _SynthesisChain.apply(f["rec_lo_rev"], f["rec_hi_rev"], mm, off, tuple(nc),
                                  tuple(n_out), a, *ds)
 
