@@ -660,7 +660,7 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
 // of an instruction (addresses dil apart) fall in distinct banks.  At the end the four waves' sums are added in
 // LDS and the workgroup writes column blockIdx.x of `partial` (n_el x gridDim.x).
 constexpr int MB_KB = 8;   // tap blocks of 16 (K <= 128)
-constexpr int MB_U = 16;   // instructions per A prefetch chunk (TT / 4 is a multiple of 4 MB_U)
+constexpr int MB_U = 8;    // instructions per A prefetch chunk (TT / 4 is a multiple of 4 MB_U)
 constexpr int MB_XR = 1;   // x window registers per thread (the first MB_XR NT samples)
 
 template <typename T>
