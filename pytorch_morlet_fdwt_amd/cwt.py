@@ -511,8 +511,7 @@ class _MorletMixFunction(torch.autograd.Function):
         dev, dt = gy.device, gy.dtype
         need_h = ctx.needs_input_grad[2]
         gH = torch.zeros_like(H) if need_h else None
-        ga = torch.zeros_like(a)
-        gb = torch.zeros_like(b)
+        gab = torch.zeros((D, a.shape[1], 2), device=dev, dtype=a.dtype)  # (ga, gb) per scale
         by_oct = {st.octave: k for k, st in enumerate(plan.stages)}
         L = _lib.lib()
         g_next = None
@@ -546,10 +545,10 @@ class _MorletMixFunction(torch.autograd.Function):
                                     _lib.ptr(ws), ws_n, rc, xj.shape[1], N, mj, S_g, st.half,
                                     grp.sup, grp.chan, st.dil, C, a.shape[1], D, r0,
                                     _lib.dtype_code(dt), _lib.stream(dev))
-                        # (rows, tiles, S_g, 2) -> per weight row d (rows are whole multiples of D)
-                        part = ws[:ws_n].view(rc, -1, S_g, 2).sum(1).view(-1, D, S_g, 2).sum(0)
-                        ga[:, idx[grp.g0:grp.g1]] += part[..., 0]
-                        gb[:, idx[grp.g0:grp.g1]] += part[..., 1]
+                        # (rows, tiles, S_g, 2) -> per weight row d (rows are whole multiples of
+                        # D): one reduction, one indexed add (the group's scales are distinct)
+                        part = ws[:ws_n].view(-1, D, ws_n // (rc * S_g * 2), S_g, 2).sum((0, 2))
+                        gab.index_add_(1, idx[grp.g0:grp.g1], part)
                         gh = _stage_backward(plan, k, grp, xj, gw, S_g, grp.local, taps,
                                              gx[r0:r1], filled, need_h, prec)
                         if gh is not None:
@@ -564,7 +563,7 @@ class _MorletMixFunction(torch.autograd.Function):
                 gx.zero_()
             g_next = gx
         gx = g_next.to(ctx.x_dtype) if ctx.needs_input_grad[0] else None
-        return gx, None, gH, ga, gb
+        return gx, None, gH, gab[..., 0], gab[..., 1]
 
 
 def morlet_mix(x: torch.Tensor, plan: MorletPlan, H: torch.Tensor, a: torch.Tensor,
@@ -682,7 +681,7 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
                         if v_pos:
                             # (rows, S_g, N): sum the nch rows of each group
                             part = ws[:ws_n].view(rc // nch, nch, S_g, N).sum(1)
-                            gV[r0 // nch:r1 // nch, gidx] += part
+                            gV[r0 // nch:r1 // nch].index_add_(1, gidx, part)
                         else:
                             part = ws[:ws_n].view(rc, -1, S_g).sum(1).view(-1, nch, S_g).sum(0)
                             gV[:, gidx] += part

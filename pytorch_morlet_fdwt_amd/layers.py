@@ -53,7 +53,9 @@ class MorletTokenMixer(nn.Module):
         dt = torch.float64 if x.dtype == torch.float64 else torch.float32
         H = self.cwt._filters(x.device, dt)
         y = morlet_mix(x.transpose(1, 2), self.cwt.plan, H, self.mag_weight, self.phase_weight)
-        y = y.transpose(1, 2) + self.bias
+        # (B, L, D) in memory order before the bias: out_proj's GEMM on a transposed view takes
+        # a much slower kernel than the copy costs
+        y = y.transpose(1, 2).contiguous() + self.bias
         return self.out_proj(y.to(x.dtype))
 
 
