@@ -534,11 +534,14 @@ __device__ inline int butterfly_index(int lane) {
 
 // One launch handles the scales [s_begin, s_end) in groups of HS (4, 2 or 1): the host
 // launches the last n_scales % 4 scales with a smaller HS, so no group computes empty scales.
+// partial holds rows from scale s_part on: tap k of scale s, channel ch, is row
+// ((s - s_part) K + k) C + ch, one column per workgroup.
 template <typename T, bool CPLX, int DIL, int HS>  // DIL: 1, 2, or 0 for any multiple of 4
 __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T* __restrict__ g,
                                                                T* __restrict__ partial,
                                                                int g_scales, int tiles,
-                                                               int s_begin, int s_end) {
+                                                               int s_begin, int s_end,
+                                                               int s_part) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int C = CPLX ? 2 : 1;
   constexpr int NV = HS * HB * C;  // sums per lane (a power of two)
@@ -637,7 +640,7 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
         const int a = j / (HB * C), b = (j / C) % HB, ch = j % C;
         const int k = k0 + b;
         if (a < ns && k < K)
-          partial[((int64_t)((s0 + a) * K + k) * C + ch) * nblocks + blockIdx.x] = v[0];
+          partial[((int64_t)((s0 + a - s_part) * K + k) * C + ch) * nblocks + blockIdx.x] = v[0];
       }
     }
   }
@@ -662,6 +665,9 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
 constexpr int MB_KB = 8;   // tap blocks of 16 (K <= 128)
 constexpr int MB_U = 8;    // instructions per A prefetch chunk (TT / 4 is a multiple of 4 MB_U)
 constexpr int MB_XR = 1;   // x window registers per thread (the first MB_XR NT samples)
+#ifndef GH_VEC_SCALES
+#define GH_VEC_SCALES 2  // trailing scale groups this small skip the matrix cores
+#endif
 
 template <typename T>
 struct Mfma16;
@@ -1763,7 +1769,8 @@ extern "C" int64_t fdwt_morlet_backward_h_workspace(int64_t rows, int64_t n_out,
 
 // The filter gradient with a workspace of workspace_elems elements.  The columns written are
 // those of the path taken (resident workgroups on the matrix cores, rows x tiles on the
-// vector kernel); a workspace smaller than that returns FDWT_ERR_SCRATCH before any launch.
+// vector kernel, each for its own scales when a stage is split between them); a workspace
+// smaller than that returns FDWT_ERR_SCRATCH before any launch.
 static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
                                  int64_t workspace_elems, void* gh, int64_t rows, int64_t n_in,
                                  int64_t n_out, int64_t x_off, int32_t n_scales, int32_t half,
@@ -1785,36 +1792,85 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
   hipStream_t hs = static_cast<hipStream_t>(stream);
   const int cs = dtype == FDWT_F64 ? 8 : 4;
   const int64_t span = TT + 2 * (int64_t)dil * half;
-  if (K <= 16 * MB_KB && rows * tiles <= INT32_MAX) {
-    // matrix-core path: launches over groups of 16 / C scales, then one column reduction
-    const int64_t total = rows * tiles;
+  const int64_t blocks = rows * tiles;
+  const size_t vlds = (size_t)(HPAD + ((span + 4 + 3) & ~3) + (int64_t)HS4 * TT * channels) * cs;
+  const bool vec_ok = (dil == 1 || dil == 2 || dil % 4 == 0) && n_el <= INT32_MAX;
+  int rc = 0;
+  // vector kernel over scales [B, E): groups of 4, the remaining 1 or 2 in one smaller group
+  // (3 stay in a group of 4, one slot idle); partial rows of scales vfirst.. at stride blocks
+  // from element vbase
+  int64_t vbase = 0;
+  int vfirst = 0;
+#define BWH_HS(TYPE, CPLX, D, S, B, E)                                                        \
+  do {                                                                                        \
+    auto k = morlet_backward_h_kernel<TYPE, CPLX, D, S>;                                      \
+    FDWT_LDS_ONCE(k);                                                                         \
+    rc = launch(k, blocks, vlds, hs, st, (const TYPE*)g, (TYPE*)workspace + vbase,            \
+                (int)g_scales, tiles, (int)(B), (int)(E), vfirst);                            \
+  } while (0)
+#define BWH_DIL(TYPE, CPLX, D, B, E)                                                          \
+  do {                                                                                        \
+    const int r4 = ((E) - (B)) % 4, m4 = r4 == 3 ? (E) : (E) - r4;                            \
+    if (m4 > (B)) BWH_HS(TYPE, CPLX, D, 4, B, m4);                                            \
+    if (!rc && (E) - m4 == 1) BWH_HS(TYPE, CPLX, D, 1, m4, E);                                \
+    if (!rc && (E) - m4 == 2) BWH_HS(TYPE, CPLX, D, 2, m4, E);                                \
+  } while (0)
+#define BWH_RANGE(TYPE, CPLX, B, E)                                                           \
+  do {                                                                                        \
+    if (dil == 1) BWH_DIL(TYPE, CPLX, 1, B, E);                                               \
+    else if (dil == 2) BWH_DIL(TYPE, CPLX, 2, B, E);                                          \
+    else BWH_DIL(TYPE, CPLX, 0, B, E);                                                        \
+  } while (0)
+  if (K <= 16 * MB_KB && blocks <= INT32_MAX) {
+    // matrix-core path: launches over groups of 16 / C scales, then one column reduction.  A
+    // trailing group of at most GH_VEC_SCALES scales goes to the vector kernel instead: a
+    // matrix-core launch costs nearly as much for one scale as for a full group.
     const int kblocks = (int)cdiv(K, 16);
     const int sk = (dil < 8 || (dil & (dil - 1))) ? 30 : __builtin_ctz(dil);
     const int64_t xs = (span + 4 - 1) + 4 * ((span + 4 - 1) >> sk) + 1;
     const size_t mlds = (size_t)std::max<int64_t>(xs, (int64_t)(NT / 64) * kblocks * 256) * cs;
     const int grp = 16 / channels;
-    int rc = 0, ncols = 1;
+    // (the split depends on the shape only, never on the workspace size)
+    int tail = n_scales % grp;
+    if (tail > GH_VEC_SCALES || !vec_ok) tail = 0;
+    const int nm = n_scales - tail;                  // scales on the matrix cores
+    const int64_t nm_el = (int64_t)nm * K * channels;  // their filter taps
+    int ncols = 0;  // partial columns of the matrix-core rows, then the vector kernel's rows
 #define GHM_KB(TYPE, CPLX, N)                                                                 \
   case N: {                                                                                   \
     auto k = morlet_grad_h_mfma_kernel<TYPE, CPLX, N>;                                        \
     FDWT_LDS_ONCE(k);                                                                         \
-    ncols = resident_blocks(k, mlds, total);                                                  \
-    if ((int64_t)ncols * n_el > workspace_elems) return FDWT_ERR_SCRATCH;                     \
-    for (int s0 = 0; s0 < n_scales && !rc; s0 += grp)                                         \
+    ncols = resident_blocks(k, mlds, blocks);                                                 \
+    if ((int64_t)ncols * nm_el + (n_el - nm_el) * blocks > workspace_elems)                   \
+      return FDWT_ERR_SCRATCH;                                                                \
+    for (int s0 = 0; s0 < nm && !rc; s0 += grp)                                               \
       rc = launch(k, ncols, mlds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,    \
-                  tiles, total, s0, std::min(n_scales, s0 + grp), sk);                        \
+                  tiles, blocks, s0, std::min(nm, s0 + grp), sk);                             \
     break;                                                                                    \
   }
 #define GHM(TYPE, CPLX)                                                                       \
   do {                                                                                        \
-    switch (kblocks) {                                                                        \
-      GHM_KB(TYPE, CPLX, 1) GHM_KB(TYPE, CPLX, 2) GHM_KB(TYPE, CPLX, 3)                       \
-      GHM_KB(TYPE, CPLX, 4) GHM_KB(TYPE, CPLX, 5) GHM_KB(TYPE, CPLX, 6)                       \
-      GHM_KB(TYPE, CPLX, 7) GHM_KB(TYPE, CPLX, 8) default: return FDWT_ERR_ARG;               \
+    if (nm > 0) {                                                                             \
+      switch (kblocks) {                                                                      \
+        GHM_KB(TYPE, CPLX, 1) GHM_KB(TYPE, CPLX, 2) GHM_KB(TYPE, CPLX, 3)                     \
+        GHM_KB(TYPE, CPLX, 4) GHM_KB(TYPE, CPLX, 5) GHM_KB(TYPE, CPLX, 6)                     \
+        GHM_KB(TYPE, CPLX, 7) GHM_KB(TYPE, CPLX, 8) default: return FDWT_ERR_ARG;             \
+      }                                                                                       \
     }                                                                                         \
-    if (rc) return rc;                                                                        \
-    return launch(reduce_cols_kernel<TYPE>, n_el, 0, hs, (const TYPE*)workspace, (TYPE*)gh,   \
+    if (!rc && tail) {                                                                        \
+      if (nm == 0 && n_el * blocks > workspace_elems) return FDWT_ERR_SCRATCH;                \
+      vbase = nm_el * ncols;                                                                  \
+      vfirst = nm;                                                                            \
+      BWH_RANGE(TYPE, CPLX, nm, n_scales);                                                    \
+    }                                                                                         \
+    if (!rc && nm > 0)                                                                        \
+      rc = launch(reduce_cols_kernel<TYPE>, nm_el, 0, hs, (const TYPE*)workspace, (TYPE*)gh,  \
                   (int64_t)ncols, (int)accumulate);                                           \
+    if (!rc && tail)                                                                          \
+      rc = launch(reduce_cols_kernel<TYPE>, n_el - nm_el, 0, hs,                              \
+                  (const TYPE*)workspace + vbase, (TYPE*)gh + nm_el, blocks,                  \
+                  (int)accumulate);                                                           \
+    return rc;                                                                                \
   } while (0)
     if (dtype == FDWT_F32) {
       if (channels == 2) GHM(float, true);
@@ -1825,35 +1881,12 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
 #undef GHM
 #undef GHM_KB
   }
-  const size_t lds = (size_t)(HPAD + ((span + 4 + 3) & ~3) + (int64_t)HS4 * TT * channels) * cs;
-  const int64_t blocks = rows * tiles;
   if (n_el > INT32_MAX) return FDWT_ERR_ARG;
   if (blocks * n_el > workspace_elems) return FDWT_ERR_SCRATCH;
-  if (dil != 1 && dil != 2 && dil % 4 != 0) return FDWT_ERR_ARG;
-  // scales [0, n4) in groups of 4; the remaining 1 or 2 in one smaller group (3 stay in a
-  // group of 4, one slot idle)
-  const int rem = n_scales % 4;
-  const int n4 = rem == 3 ? n_scales : n_scales - rem;
-  int rc = 0;
-#define BWH_HS(TYPE, CPLX, D, S, B, E)                                                        \
-  do {                                                                                        \
-    auto k = morlet_backward_h_kernel<TYPE, CPLX, D, S>;                                      \
-    FDWT_LDS_ONCE(k);                                                                         \
-    rc = launch(k, blocks, lds, hs, st, (const TYPE*)g, (TYPE*)workspace, (int)g_scales,      \
-                tiles, (int)(B), (int)(E));                                                   \
-  } while (0)
-#define BWH_DIL(TYPE, CPLX, D)                                                                \
-  do {                                                                                        \
-    if (n4 > 0) BWH_HS(TYPE, CPLX, D, 4, 0, n4);                                              \
-    if (rc) return rc;                                                                        \
-    if (n4 < n_scales && n_scales - n4 == 1) BWH_HS(TYPE, CPLX, D, 1, n4, n_scales);          \
-    if (n4 < n_scales && n_scales - n4 == 2) BWH_HS(TYPE, CPLX, D, 2, n4, n_scales);          \
-  } while (0)
+  if (!vec_ok) return FDWT_ERR_ARG;
 #define BWH(TYPE, CPLX)                                                                       \
   do {                                                                                        \
-    if (dil == 1) BWH_DIL(TYPE, CPLX, 1);                                                     \
-    else if (dil == 2) BWH_DIL(TYPE, CPLX, 2);                                                \
-    else BWH_DIL(TYPE, CPLX, 0);                                                              \
+    BWH_RANGE(TYPE, CPLX, 0, n_scales);                                                       \
     if (rc) return rc;                                                                        \
     return launch(reduce_cols_kernel<TYPE>, n_el, 0, hs, (const TYPE*)workspace, (TYPE*)gh,   \
                   blocks, (int)accumulate);                                                   \
@@ -1865,6 +1898,7 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
   if (channels == 2) BWH(double, true);
   BWH(double, false);
 #undef BWH
+#undef BWH_RANGE
 #undef BWH_DIL
 #undef BWH_HS
 }

@@ -64,11 +64,14 @@ def _both(R, n_out, sup, half, dil, C, margin, acc, dtype, seed):
 PAIRS = [
     ((512, 3000, [20, 33, 40, 40], 40, 1, 2, 100, 0), (3, 700, [5, 9], 9, 4, 2, 30, 1)),
     ((96, 2100, [55, 70], 70, 8, 2, 600, 1), (5, 300, [12], 12, 2, 1, 0, 0)),  # K = 141: vector
+    # 8 + 1 and 16 + 2 scales: matrix cores, then the vector kernel for the trailing group
+    ((64, 2000, [4, 5, 6, 7, 8, 9, 10, 11, 12], 12, 4, 2, 30, 1),
+     (3, 700, [1 + s * 9 // 17 for s in range(18)], 10, 2, 1, 0, 0)),
 ]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
-@pytest.mark.parametrize("pair", PAIRS, ids=["mfma", "vector"])
+@pytest.mark.parametrize("pair", PAIRS, ids=["mfma", "vector", "split"])
 def test_noalloc_filter_gradient_matches_workspace_entry(pair, dtype):
     for k, case in enumerate(pair):
         print(f"noalloc case {k}: {case} {dtype}", flush=True)
