@@ -27,8 +27,9 @@ extern "C" {
 #define FDWT_F16 2
 #define FDWT_BF16 3
 /* fp32 storage with bf16 matrix-core operands and fp32 accumulation (the reference's "bf16"
- * precision, conv.py:332-338): accepted by fdwt_morlet_backward_x and fdwt_morlet_backward_h;
- * where no bf16 kernel applies they compute in fp32 */
+ * precision, conv.py:332-338): accepted by fdwt_morlet_backward_x (matrix-core adjoint) and
+ * fdwt_morlet_backward_h (matrix-core filter gradient); stages that run on the vector kernels
+ * compute in fp32 */
 #define FDWT_F32_BF16 4
 
 /* boundary modes, numbered as the reference's MODES table (kernels/dwt.py:30) */

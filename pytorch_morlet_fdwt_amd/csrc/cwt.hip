@@ -646,6 +646,14 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
   }
 }
 
+// float -> bf16 bits, round to nearest even (NaN stays a NaN)
+__device__ inline uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
 // ------------------------------------------------------------------ filter gradient, MFMA
 // The same partial sums as a matrix product on the matrix cores:
 //     gh[(s, ch)][k] = sum_n G[(s, ch)][n] X[n][k],   X[n][k] = x[n + x_off - dil (k - half)]
@@ -662,6 +670,12 @@ __global__ void __launch_bounds__(NT) morlet_backward_h_kernel(Stage st, const T
 // samples) is staged in LDS with four words of skew per dil words (dil >= 8), so the 16 taps
 // of an instruction (addresses dil apart) fall in distinct banks.  At the end the four waves' sums are added in
 // LDS and the workgroup writes column blockIdx.x of `partial` (n_el x gridDim.x).
+// With BF (fp32 storage, the reference's "bf16" precision, conv.py:372-408) both operands are
+// rounded to bf16 (round to nearest even, v_cvt_pk_bf16_f32) and each
+// v_mfma_f32_16x16x16_bf16 takes 16 positions: lane l supplies
+// A[l % 16][4 (l / 16) + v] and B[4 (l / 16) + v][l % 16], v < 4 (four consecutive positions,
+// which never straddle a skew step: the skew period dil is a multiple of 8), with the same
+// result layout; sums stay fp32.
 constexpr int MB_KB = 8;   // tap blocks of 16 (K <= 128)
 constexpr int MB_U = 8;    // instructions per A prefetch chunk (TT / 4 is a multiple of 4 MB_U)
 constexpr int MB_XR = 1;   // x window registers per thread (the first MB_XR NT samples)
@@ -688,7 +702,7 @@ struct Mfma16<double> {
   static __device__ inline int row(int lane, int e) { return lane / 16 + 4 * e; }
 };
 
-template <typename T, bool CPLX, int KB>  // KB = ceil(K / 16) tap blocks
+template <typename T, bool CPLX, int KB, bool BF>  // KB = ceil(K / 16) tap blocks
 __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const T* __restrict__ g,
                                                                 T* __restrict__ partial,
                                                                 int g_scales, int tiles,
@@ -746,9 +760,13 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
     return q;
   };
   T an[MB_U], xr[MB_XR];
+  // position of prefetch slot u of a chunk starting at c0 (this lane's A elements)
+  auto a_pos = [&](int c0, int u) {
+    return BF ? c0 + 16 * (u / 4) + 4 * kpos + (u % 4) : c0 + 4 * u + kpos;
+  };
   auto load_a = [&](const Tile& q, int c0) {
 #pragma unroll
-    for (int u = 0; u < MB_U; ++u) an[u] = q.grow[(int64_t)min(c0 + 4 * u + kpos, q.nvalid - 1) * C];
+    for (int u = 0; u < MB_U; ++u) an[u] = q.grow[(int64_t)min(a_pos(c0, u), q.nvalid - 1) * C];
   };
   auto load_x = [&](const Tile& q) {
 #pragma unroll
@@ -784,6 +802,30 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
     wave_range(nxt.nvalid, nbeg, nend);
     if (pbeg >= pend) load_a(nxt, nbeg);  // no positions of this tile for this wave
     for (int c0 = pbeg; c0 < pend; c0 += 4 * MB_U) {
+      if constexpr (BF) {
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        v4s a4[MB_U / 4];
+#pragma unroll
+        for (int u = 0; u < MB_U; ++u)
+          a4[u / 4][u % 4] = __builtin_bit_cast(
+              short, (__bf16)((arow_ok && a_pos(c0, u) < nvalid) ? (float)an[u] : 0.f));
+        const bool last = c0 + 4 * MB_U >= pend;
+        load_a(last ? nxt : cur_t, last ? nbeg : c0 + 4 * MB_U);
+#pragma unroll
+        for (int u2 = 0; u2 < MB_U / 4; ++u2) {
+          const T* xp = X + skew(c0 + 16 * u2 + 4 * kpos);
+          v4s b[KB];
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              b[kb][v] = __builtin_bit_cast(short, (__bf16)(float)xp[boff[kb] + v]);
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+            acc[kb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a4[u2], b[kb], acc[kb], 0, 0, 0);
+        }
+        continue;
+      }
       T cur[MB_U];
 #pragma unroll
       for (int u = 0; u < MB_U; ++u)
@@ -883,14 +925,6 @@ __host__ __device__ inline int ma_fl(int half, bool bf = false) { return 2 * hal
 // both in the operand type
 __host__ __device__ inline int64_t ma_lds(int half, int C, int es, bool bf) {
   return (int64_t)C * (16 * ma_ws(half, bf) + ma_fl(half, bf)) * (bf ? 2 : es);
-}
-
-// float -> bf16 bits, round to nearest even (NaN stays a NaN)
-__device__ inline uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
 }
 
 // One g position (C values, re then im) through a buffer resource; 0 outside its range.
@@ -1780,7 +1814,9 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
   Stage st;
   int e = fill_stage(st, x, g, n_in, n_out, x_off, n_scales, half, support, chan, dil, channels);
   if (e) return e;
-  if (dtype == FDWT_F32_BF16) dtype = FDWT_F32;  // no bf16 kernel here: fp32 operands
+  // bf16 operands on the matrix-core path; the vector kernel computes in fp32
+  const bool bf = dtype == FDWT_F32_BF16;
+  if (bf) dtype = FDWT_F32;
   if (!workspace || !gh || rows < 0 || (dtype != FDWT_F32 && dtype != FDWT_F64)) return FDWT_ERR_ARG;
   for (int s = 0; s < n_scales; ++s)
     if (chan[s] >= g_scales) return FDWT_ERR_ARG;
@@ -1838,7 +1874,7 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
     int ncols = 0;  // partial columns of the matrix-core rows, then the vector kernel's rows
 #define GHM_KB(TYPE, CPLX, N)                                                                 \
   case N: {                                                                                   \
-    auto k = morlet_grad_h_mfma_kernel<TYPE, CPLX, N>;                                        \
+    auto k = morlet_grad_h_mfma_kernel<TYPE, CPLX, N, BFV>;                                   \
     FDWT_LDS_ONCE(k);                                                                         \
     ncols = resident_blocks(k, mlds, blocks);                                                 \
     if ((int64_t)ncols * nm_el + (n_el - nm_el) * blocks > workspace_elems)                   \
@@ -1872,6 +1908,12 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
                   (int)accumulate);                                                           \
     return rc;                                                                                \
   } while (0)
+    if (dtype == FDWT_F32 && bf) {
+      constexpr bool BFV = true;
+      if (channels == 2) GHM(float, true);
+      GHM(float, false);
+    }
+    constexpr bool BFV = false;
     if (dtype == FDWT_F32) {
       if (channels == 2) GHM(float, true);
       GHM(float, false);

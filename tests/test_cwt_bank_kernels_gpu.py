@@ -167,3 +167,54 @@ def test_bank_adjoint_bf16_operands(case):
     torch.testing.assert_close(got, ref_bf, rtol=0, atol=1e-5 * scale)
     err = (got - ref).abs().max().item() / ref.abs().max().item()
     assert err < 1e-2, err
+
+
+# stages whose filter gradient runs on the matrix cores (K = 2 half + 1 <= 128)
+GH_BF16_CASES = [c for c in CASES if 2 * c[1] + 1 <= 128]
+
+
+@pytest.mark.parametrize("case", GH_BF16_CASES,
+                         ids=[f"d{c[0]}h{c[1]}C{c[3]}m{c[4]}" for c in GH_BF16_CASES])
+def test_filter_gradient_bf16_operands(case):
+    """FDWT_F32_BF16 for the filter gradient (the reference's "bf16" precision for backward_h,
+    conv.py:372-408): on the matrix cores g and x are rounded to bf16 and the products summed
+    in fp32.  Those scales must match the tap gradient of the bf16-rounded operands computed in
+    float64 to fp32 accumulation (1e-5 of the largest value) and the exact gradient to the
+    mode's ~5e-3 (README.md:206-212); a trailing group of one or two scales that the launch
+    gives to the vector kernel keeps fp32 operands and the fp32 bar."""
+    dil, half, sup, C, margin, _ = case
+    R, n_out, S, g_scales = 3, 700, len(sup), len(sup) + 2
+    chan = [(2 * s + 1) % g_scales for s in range(S)]
+    n_in, x_off = n_out + 2 * margin, margin
+    gen = torch.Generator().manual_seed(dil * 1000 + half + 11)
+    f64 = torch.float64
+    x = torch.randn(R, n_in, dtype=f64, generator=gen).float()
+    g = torch.randn(R, g_scales, n_out, C, dtype=f64, generator=gen).float()
+    bf = lambda t: t.to(torch.bfloat16).double()  # noqa: E731
+    ref_bf = _tap_gradient(bf(x), bf(g)[:, chan], half, dil, x_off, n_out)
+    ref = _tap_gradient(x.double(), g.double()[:, chan], half, dil, x_off, n_out)
+    L = _lib.lib()
+    ws_n = L.fdwt_morlet_backward_h_workspace(R, n_out, S, half, C)
+    ws = torch.empty(max(1, ws_n), device=DEV)
+    gh = torch.full((S, 2 * half + 1, C), float("nan"), device=DEV)
+    xd, gd = x.to(DEV).contiguous(), g.to(DEV).contiguous()
+    _lib.launch("fdwt_morlet_backward_h", torch.device(DEV), _lib.ptr(xd), _lib.ptr(gd),
+                _lib.ptr(ws), ws_n, _lib.ptr(gh), R, n_in, n_out, x_off, S, half, _i32(sup),
+                _i32(chan), dil, C, g_scales, 0, _lib.F32_BF16, _lib.stream(torch.device(DEV)))
+    torch.cuda.synchronize()
+    got = gh.cpu().double()
+    assert torch.isfinite(got).all()
+    # the launch's split: groups of 16 / C scales on the matrix cores; a trailing group of at
+    # most two scales on the vector kernel when the dilation allows it (1, 2 or a multiple of 4)
+    grp = 16 // C
+    tail = S % grp
+    if tail > 2 or not (dil in (1, 2) or dil % 4 == 0):
+        tail = 0
+    nm = S - tail
+    scale = ref_bf.abs().max().item()
+    if nm:
+        torch.testing.assert_close(got[:nm], ref_bf[:nm], rtol=0, atol=1e-5 * scale)
+        err = (got[:nm] - ref[:nm]).abs().max().item() / ref.abs().max().item()
+        assert err < 1e-2, err
+    if tail:
+        torch.testing.assert_close(got[nm:], ref[nm:], rtol=0, atol=2e-5 * scale)

@@ -271,14 +271,17 @@ def test_attention_fp32_and_bf16_run():
 
 def test_bf16_precision_mode_backward(monkeypatch):
     """config.allow_bf16 (the reference's "bf16" precision: bf16 matrix operands, fp32
-    accumulation, README.md:206-212) rounds the bank adjoint's operands -- the upstream
-    scalogram gradient and the filters -- to bf16.  CWT: the input gradient matches the
-    float64 oracle gradient with exactly those operands rounded to bf16 (a CPU emulation of the
-    mode) to 2e-3 relative L2 error, while both miss the exact gradient by ~1.6e-2 (the mode's
-    own error on this problem: oscillatory filters against a wideband gradient cancel).
-    MorletAttention: forward outputs and parameter gradients unchanged (those kernels compute
-    in fp32), the input gradient within 8e-2 relative L2 error of float64 (4.6e-2 measured),
-    and bf16 inputs, which select the mode (cwt.py:540), within 1e-1 (6.1e-2 measured)."""
+    accumulation, README.md:206-212) rounds the operands of the bank adjoint -- the upstream
+    scalogram gradient and the filters -- and of the matrix-core filter gradient -- the
+    upstream gradient and the signal -- to bf16.  CWT: the input gradient matches the float64
+    oracle gradient with exactly those operands rounded to bf16 (a CPU emulation of the mode)
+    to 2e-3 relative L2 error, while both miss the exact gradient by ~1.6e-2 (the mode's own
+    error on this problem: oscillatory filters against a wideband gradient cancel).
+    MorletAttention: forward outputs and the mixing weights' gradient unchanged (those kernels
+    compute in fp32), the input gradient within 8e-2 relative L2 error of float64 (4.6e-2
+    measured), the scale parameters' gradient (through the filter gradient) within 5e-2
+    (2.4e-2 measured), and bf16 inputs, which select the mode (cwt.py:540), within 1e-1 (6.1e-2
+    and 4.2e-2 measured)."""
     def rel(a, b):
         return ((a - b).norm() / b.norm()).item()
 
@@ -326,10 +329,12 @@ def test_bf16_precision_mode_backward(monkeypatch):
 
     r64, r32, rb, rbf = (run(torch.float64, False), run(torch.float32, False),
                          run(torch.float32, True), run(torch.bfloat16, False))
-    assert torch.equal(rb[0], r32[0]) and torch.equal(rb[2], r32[2]) and torch.equal(rb[3], r32[3])
+    assert torch.equal(rb[0], r32[0]) and torch.equal(rb[2], r32[2])
     assert 1e-6 < rel(rb[1], r64[1]) < 8e-2, rel(rb[1], r64[1])
-    assert torch.isfinite(rbf[1]).all()
+    assert 1e-4 < rel(rb[3], r64[3]) < 5e-2, rel(rb[3], r64[3])
+    assert torch.isfinite(rbf[1]).all() and torch.isfinite(rbf[3]).all()
     assert rel(rbf[1], r64[1]) < 1e-1, rel(rbf[1], r64[1])
+    assert rel(rbf[3], r64[3]) < 1e-1, rel(rbf[3], r64[3])
 
 
 def test_fp32_attention_matches_fp64():
