@@ -212,6 +212,22 @@ def attention_gpu(steps, warmup, dev, shape=ATT_SHAPE, channel_mix=False):
                          "frac": fl / (ms * 1e-3) / FP32_PEAK, "alg_flops": fl}}
 
 
+def bf16_mode(leg, *args):
+    """The same leg with ``config.allow_bf16`` set (the reference's "bf16" precision: bf16
+    matrix-core operands with fp32 accumulation in the bank adjoint and filter gradient): its
+    step time and throughput, reported beside the fp32 line (a mode the reference offers for
+    speed, not the headline's arithmetic)."""
+    import pytorch_morlet_fdwt_amd as fdwt
+    saved = fdwt.config.allow_bf16
+    fdwt.config.allow_bf16 = True
+    try:
+        r = leg(*args)
+    finally:
+        fdwt.config.allow_bf16 = saved
+    return {"ms_per_step": r["ms_per_step"], "value": r["value"], "unit": r["unit"],
+            "precision": "bf16 operands, fp32 accumulation (config.allow_bf16)"}
+
+
 def attention_cpu(batch=1, reps=3, channel_mix=False):
     """The oracle (reference CPU fallback restated, fp32) on a batch-`batch` sample."""
     from oracle import cwt as O
@@ -590,6 +606,7 @@ def main():
     }
     if not a.no_attention:
         att = attention_gpu(max(3, a.steps // 2), a.warmup, dev)
+        att["bf16_mode"] = bf16_mode(attention_gpu, max(3, a.steps // 2), a.warmup, dev)
         if not a.no_cpu_baseline:
             att["cpu_baseline"] = attention_cpu()
         line["morlet_attention"] = att
@@ -604,6 +621,7 @@ def main():
         line["token_mixer_cfg4"] = token_mixer_cfg4(k, a.warmup, dev, cpu)
         line["dwt_cfg1"] = dwt_cfg1(k, a.warmup, dev, cpu)
         scaled = attention_gpu(2, 1, dev, ATT_SCALED)
+        scaled["bf16_mode"] = bf16_mode(attention_gpu, 2, 1, dev, ATT_SCALED)
         scaled["cpu_baseline"] = None  # the CPU oracle needs minutes per step at this size
         line["morlet_attention_scaled"] = scaled
     if not a.no_cpu_baseline:

@@ -1866,9 +1866,11 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
     const int64_t xs = (span + 4 - 1) + 4 * ((span + 4 - 1) >> sk) + 1;
     const size_t mlds = (size_t)std::max<int64_t>(xs, (int64_t)(NT / 64) * kblocks * 256) * cs;
     const int grp = 16 / channels;
-    // (the split depends on the shape only, never on the workspace size)
+    // (the split depends on the shape and operand precision only, never on the workspace
+    // size; with bf16 operands a whole group on the matrix cores costs less than one or two
+    // scales on the vector kernel, so nothing goes there)
     int tail = n_scales % grp;
-    if (tail > GH_VEC_SCALES || !vec_ok) tail = 0;
+    if (tail > GH_VEC_SCALES || !vec_ok || bf) tail = 0;
     const int nm = n_scales - tail;                  // scales on the matrix cores
     const int64_t nm_el = (int64_t)nm * K * channels;  // their filter taps
     int ncols = 0;  // partial columns of the matrix-core rows, then the vector kernel's rows

@@ -180,8 +180,8 @@ def test_filter_gradient_bf16_operands(case):
     conv.py:372-408): on the matrix cores g and x are rounded to bf16 and the products summed
     in fp32.  Those scales must match the tap gradient of the bf16-rounded operands computed in
     float64 to fp32 accumulation (1e-5 of the largest value) and the exact gradient to the
-    mode's ~5e-3 (README.md:206-212); a trailing group of one or two scales that the launch
-    gives to the vector kernel keeps fp32 operands and the fp32 bar."""
+    mode's ~5e-3 (README.md:206-212).  With bf16 operands every scale runs on the matrix cores
+    (no trailing group on the vector kernel)."""
     dil, half, sup, C, margin, _ = case
     R, n_out, S, g_scales = 3, 700, len(sup), len(sup) + 2
     chan = [(2 * s + 1) % g_scales for s in range(S)]
@@ -204,17 +204,7 @@ def test_filter_gradient_bf16_operands(case):
     torch.cuda.synchronize()
     got = gh.cpu().double()
     assert torch.isfinite(got).all()
-    # the launch's split: groups of 16 / C scales on the matrix cores; a trailing group of at
-    # most two scales on the vector kernel when the dilation allows it (1, 2 or a multiple of 4)
-    grp = 16 // C
-    tail = S % grp
-    if tail > 2 or not (dil in (1, 2) or dil % 4 == 0):
-        tail = 0
-    nm = S - tail
     scale = ref_bf.abs().max().item()
-    if nm:
-        torch.testing.assert_close(got[:nm], ref_bf[:nm], rtol=0, atol=1e-5 * scale)
-        err = (got[:nm] - ref[:nm]).abs().max().item() / ref.abs().max().item()
-        assert err < 1e-2, err
-    if tail:
-        torch.testing.assert_close(got[nm:], ref[nm:], rtol=0, atol=2e-5 * scale)
+    torch.testing.assert_close(got, ref_bf, rtol=0, atol=1e-5 * scale)
+    err = (got - ref).abs().max().item() / ref.abs().max().item()
+    assert err < 1e-2, err

@@ -280,8 +280,8 @@ def test_bf16_precision_mode_backward(monkeypatch):
     MorletAttention: forward outputs and the mixing weights' gradient unchanged (those kernels
     compute in fp32), the input gradient within 8e-2 relative L2 error of float64 (4.6e-2
     measured), the scale parameters' gradient (through the filter gradient) within 5e-2
-    (2.4e-2 measured), and bf16 inputs, which select the mode (cwt.py:540), within 1e-1 (6.1e-2
-    and 4.2e-2 measured)."""
+    (3.4e-2 measured), and bf16 inputs, which select the mode (cwt.py:540), within 1e-1 (6.1e-2
+    and 4.5e-2 measured)."""
     def rel(a, b):
         return ((a - b).norm() / b.norm()).item()
 
