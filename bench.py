@@ -589,6 +589,9 @@ def main():
                 "alg_bytes_per_launch": kernels[dom]["alg_bytes"],
                 "mean_launch_ms": kernels[dom]["mean_ms"]}
 
+    # the same step captured once in a HIP graph and replayed: its 80 dependent launches
+    # without the host's launch work between them (reported beside the eager value)
+    gms = _graph_timed(lambda: step_gpu(fdwt, data, grads), a.steps)
     line = {
         "metric": "wavedec+waverec fwd+bwd GB/s (algorithmic HBM bytes / step time)",
         "value": value, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -603,6 +606,10 @@ def main():
                    "modes": list(MODES), "level": LEVEL, "parallelism": "single GPU"},
         "roofline": roofline,
         "kernels": kernels,
+        "graph": {"ms_per_step": gms, "value": total / (gms * 1e-3) / 1e9,
+                  "note": "the same 20-combination step captured once in a HIP graph "
+                          "(torch.cuda.graph) and replayed: kernel time without the host's "
+                          "launch work"},
     }
     if not a.no_attention:
         att = attention_gpu(max(3, a.steps // 2), a.warmup, dev)
