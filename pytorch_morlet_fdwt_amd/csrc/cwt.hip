@@ -702,7 +702,7 @@ struct Mfma16<double> {
   static __device__ inline int row(int lane, int e) { return lane / 16 + 4 * e; }
 };
 
-template <typename T, bool CPLX, int KB, bool BF>  // KB = ceil(K / 16) tap blocks
+template <typename T, bool CPLX, int KB, bool BF, bool LIN>  // KB = ceil(K / 16) tap blocks
 __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const T* __restrict__ g,
                                                                 T* __restrict__ partial,
                                                                 int g_scales, int tiles,
@@ -713,7 +713,9 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
   typedef typename Mfma16<T>::v4 v4;
   constexpr int C = CPLX ? 2 : 1;
   T* const X = reinterpret_cast<T*>(smem_raw);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // (the wave index made visibly wave-uniform: chunk bounds, the tile choice and with it the
+  // A buffer resource stay in scalar registers)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = st.half, dil = st.dil, K = 2 * half + 1;
   const int span = TT + 2 * dil * half + 4;
   const int ns = s_end - s_begin;
@@ -744,30 +746,47 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
     b = min(wave * per, nvalid);
     e = min(b + per, nvalid);
   };
+  // A comes through a buffer resource per tile whose base is the tile's first position in the
+  // row's block of g (wave-uniform); a lane's 32-bit offset selects its scale row and channel,
+  // and the slots of a chunk differ by constants (immediate offsets).  The host keeps every
+  // offset below 2^31; the resource ends with g, so reads past a row's last valid position
+  // return finite data of g or 0, and are masked below.  Rows of scales >= ns load row 0 and
+  // are never masked: their result rows are discarded.
   struct Tile {
-    const T* grow;  // g of this lane's A row at the tile's first position
+    BufRsrc ga;     // g from the tile's first position of the row block
     const T* xrow;
     int64_t xb;     // x index of window element 0
     int nvalid;
   };
+  const int64_t g_elems = (total / tiles) * g_scales * st.n_out * C;
   auto tile_of = [&](int64_t t) {
     Tile q;
     const int64_t row = t / tiles, n0 = (t % tiles) * (int64_t)TT;
-    q.grow = g + ((row * g_scales + chan_a) * st.n_out + n0) * C + ach;
+    const int64_t e0 = row * g_scales * st.n_out * C + n0 * C;
+    q.ga = make_rsrc(g + e0, min((g_elems - e0) * (int64_t)sizeof(T), (int64_t)INT32_MAX));
     q.xrow = static_cast<const T*>(st.x) + row * st.n_in;
     q.xb = n0 + st.x_off - (int64_t)dil * half;
     q.nvalid = (int)min((int64_t)TT, st.n_out - n0);
     return q;
   };
   T an[MB_U], xr[MB_XR];
-  // position of prefetch slot u of a chunk starting at c0 (this lane's A elements)
+  // position of prefetch slot u of a chunk starting at c0 (this lane's A elements), and the
+  // lane's part of it
   auto a_pos = [&](int c0, int u) {
     return BF ? c0 + 16 * (u / 4) + 4 * kpos + (u % 4) : c0 + 4 * u + kpos;
   };
+  const int a_lane =
+      (int)(((int64_t)chan_a * st.n_out + (BF ? 4 : 1) * kpos) * C + ach) * (int)sizeof(T);
   auto load_a = [&](const Tile& q, int c0) {
+    const int voff = a_lane + c0 * C * (int)sizeof(T);
 #pragma unroll
-    for (int u = 0; u < MB_U; ++u) an[u] = q.grow[(int64_t)min(a_pos(c0, u), q.nvalid - 1) * C];
+    for (int u = 0; u < MB_U; ++u)
+      an[u] = buf_load<T>(q.ga, voff + (a_pos(0, u) - a_pos(0, 0)) * C * (int)sizeof(T));
   };
+  // B addresses (LIN, chosen by the host when sk >= 5): within a chunk (32 positions from a
+  // multiple of 32) the skewed index is linear when the skew period dil is >= 32 or there is
+  // no skew, so the slots' LDS reads differ by constants (immediate offsets) from one address
+  // per tap block
   auto load_x = [&](const Tile& q) {
 #pragma unroll
     for (int r = 0; r < MB_XR; ++r)
@@ -802,18 +821,21 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
     wave_range(nxt.nvalid, nbeg, nend);
     if (pbeg >= pend) load_a(nxt, nbeg);  // no positions of this tile for this wave
     for (int c0 = pbeg; c0 < pend; c0 += 4 * MB_U) {
+      // positions >= nvalid (a row's last tile only) get a zero A element
+      const bool full = c0 + 4 * MB_U <= nvalid;
       if constexpr (BF) {
         typedef short v4s __attribute__((ext_vector_type(4)));
         v4s a4[MB_U / 4];
 #pragma unroll
         for (int u = 0; u < MB_U; ++u)
           a4[u / 4][u % 4] = __builtin_bit_cast(
-              short, (__bf16)((arow_ok && a_pos(c0, u) < nvalid) ? (float)an[u] : 0.f));
+              short, (__bf16)((full || a_pos(c0, u) < nvalid) ? (float)an[u] : 0.f));
         const bool last = c0 + 4 * MB_U >= pend;
         load_a(last ? nxt : cur_t, last ? nbeg : c0 + 4 * MB_U);
+        const int xl = skew(c0 + 4 * kpos);
 #pragma unroll
         for (int u2 = 0; u2 < MB_U / 4; ++u2) {
-          const T* xp = X + skew(c0 + 16 * u2 + 4 * kpos);
+          const T* xp = LIN ? X + (xl + 16 * u2) : X + skew(c0 + 16 * u2 + 4 * kpos);
           v4s b[KB];
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb)
@@ -827,26 +849,36 @@ __global__ void __launch_bounds__(NT) morlet_grad_h_mfma_kernel(Stage st, const 
         continue;
       }
       T cur[MB_U];
+      if (full) {
 #pragma unroll
-      for (int u = 0; u < MB_U; ++u)
-        cur[u] = (arow_ok && c0 + 4 * u + kpos < nvalid) ? an[u] : T(0);
+        for (int u = 0; u < MB_U; ++u) cur[u] = an[u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < MB_U; ++u) cur[u] = c0 + 4 * u + kpos < nvalid ? an[u] : T(0);
+      }
       const bool last = c0 + 4 * MB_U >= pend;
       load_a(last ? nxt : cur_t, last ? nbeg : c0 + 4 * MB_U);
       // B values: the LDS reads of step u + 1 are issued before the instructions of step u,
       // so an instruction never waits for its own read (fences keep that order; without them
       // the compiler reuses one register and puts a full LDS wait before every instruction)
-      T bc[KB], bn[KB];
-      {
-        const T* xp = X + skew(c0 + kpos);
+      const T* xl[KB];  // LIN: slot u of tap block kb reads xl[kb][4 u]
+      const int x0 = skew(c0 + kpos);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) bc[kb] = xp[boff[kb]];
-      }
+      for (int kb = 0; kb < KB; ++kb) xl[kb] = X + (x0 + boff[kb]);
+      T bc[KB], bn[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) bc[kb] = xl[kb][0];
 #pragma unroll
       for (int u = 0; u < MB_U; ++u) {
         if (u + 1 < MB_U) {
-          const T* xp = X + skew(c0 + 4 * (u + 1) + kpos);
+          if constexpr (LIN) {
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) bn[kb] = xp[boff[kb]];
+            for (int kb = 0; kb < KB; ++kb) bn[kb] = xl[kb][4 * (u + 1)];
+          } else {
+            const T* xp = X + skew(c0 + 4 * (u + 1) + kpos);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) bn[kb] = xp[boff[kb]];
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1857,7 +1889,9 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
     else if (dil == 2) BWH_DIL(TYPE, CPLX, 2, B, E);                                          \
     else BWH_DIL(TYPE, CPLX, 0, B, E);                                                        \
   } while (0)
-  if (K <= 16 * MB_KB && blocks <= INT32_MAX) {
+  // (the matrix-core kernel reads g at 32-bit byte offsets within a row block of g_scales rows)
+  const bool a_off_ok = ((int64_t)g_scales * n_out + TT + 64) * channels * cs <= INT32_MAX;
+  if (K <= 16 * MB_KB && blocks <= INT32_MAX && a_off_ok) {
     // matrix-core path: launches over groups of 16 / C scales, then one column reduction.  A
     // trailing group of at most GH_VEC_SCALES scales goes to the vector kernel instead: a
     // matrix-core launch costs nearly as much for one scale as for a full group.
@@ -1876,8 +1910,11 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
     int ncols = 0;  // partial columns of the matrix-core rows, then the vector kernel's rows
 #define GHM_KB(TYPE, CPLX, N)                                                                 \
   case N: {                                                                                   \
-    auto k = morlet_grad_h_mfma_kernel<TYPE, CPLX, N, BFV>;                                   \
-    FDWT_LDS_ONCE(k);                                                                         \
+    auto k0 = morlet_grad_h_mfma_kernel<TYPE, CPLX, N, BFV, false>;                           \
+    auto k1 = morlet_grad_h_mfma_kernel<TYPE, CPLX, N, BFV, true>;                            \
+    FDWT_LDS_ONCE(k0);                                                                        \
+    FDWT_LDS_ONCE(k1);                                                                        \
+    auto k = sk >= 5 ? k1 : k0;                                                               \
     ncols = resident_blocks(k, mlds, blocks);                                                 \
     if ((int64_t)ncols * nm_el + (n_el - nm_el) * blocks > workspace_elems)                   \
       return FDWT_ERR_SCRATCH;                                                                \
