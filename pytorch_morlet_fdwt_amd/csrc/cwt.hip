@@ -680,7 +680,7 @@ constexpr int MB_KB = 8;   // tap blocks of 16 (K <= 128)
 constexpr int MB_U = 8;    // instructions per A prefetch chunk (TT / 4 is a multiple of 4 MB_U)
 constexpr int MB_XR = 1;   // x window registers per thread (the first MB_XR NT samples)
 #ifndef GH_VEC_SCALES
-#define GH_VEC_SCALES 2  // trailing scale groups this small skip the matrix cores
+#define GH_VEC_SCALES 1  // trailing scale groups this small skip the matrix cores
 #endif
 
 template <typename T>
@@ -1894,7 +1894,9 @@ static int morlet_backward_h_run(const void* x, const void* g, void* workspace,
   if (K <= 16 * MB_KB && blocks <= INT32_MAX && a_off_ok) {
     // matrix-core path: launches over groups of 16 / C scales, then one column reduction.  A
     // trailing group of at most GH_VEC_SCALES scales goes to the vector kernel instead: a
-    // matrix-core launch costs nearly as much for one scale as for a full group.
+    // matrix-core launch costs nearly as much for one scale as for a full group (measured:
+    // one scale costs the vector kernel about half a matrix-core launch, two scales as much
+    // as or, at dilations 1 and 2 on long rows, 1.4x a matrix-core launch).
     const int kblocks = (int)cdiv(K, 16);
     const int sk = (dil < 8 || (dil & (dil - 1))) ? 30 : __builtin_ctz(dil);
     const int64_t xs = (span + 4 - 1) + 4 * ((span + 4 - 1) >> sk) + 1;

@@ -64,8 +64,9 @@ CASES = [
     (64, 20, [10, 20], 2, 1400, 1),
     (64, 38, [38], 1, 2500, 0),
     (128, 9, [5, 9], 2, 1300, 0),     # dilation above 64: residue groups of at most 64
-    # more scales than one matrix-core group of 16 / C: the trailing 1 or 2 on the vector
-    # kernel, its partial sums after the matrix-core ones in the same workspace
+    # more scales than one matrix-core group of 16 / C: a trailing single scale (9 = 8 + 1) on
+    # the vector kernel, its partial sums after the matrix-core ones in the same workspace;
+    # 18 = 16 + 2: a second, partly filled matrix-core group
     (4, 12, [4, 5, 6, 7, 8, 9, 10, 11, 12], 2, 30, 1),
     (2, 10, [1 + s * 9 // 17 for s in range(18)], 1, 0, 0),
 ]
