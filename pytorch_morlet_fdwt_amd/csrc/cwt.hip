@@ -1278,12 +1278,17 @@ struct SoftArgs {
   double inv_tau;
 };
 
+// The V row of a workgroup's signal row (the division by nch once per workgroup, not per
+// scale and position): per channel, V[(r % nch)][.]; per position, the (S_total, N) plane of
+// group r / nch.
 template <typename T>
-__device__ inline T v_value(const SoftArgs& sa, const T* V, int64_t row, int gs, int64_t n,
-                            int64_t n_out) {
+__device__ inline const T* v_row(const SoftArgs& sa, const T* V, int64_t row, int64_t n_out) {
   const int64_t r = row + sa.row0;
-  if (sa.v_pos) return V[((r / sa.nch) * sa.s_total + gs) * n_out + n];
-  return V[(r % sa.nch) * sa.s_total + gs];
+  return sa.v_pos ? V + (r / sa.nch) * sa.s_total * n_out : V + (r % sa.nch) * sa.s_total;
+}
+template <typename T>
+__device__ inline T v_value(const SoftArgs& sa, const T* vrow, int gs, int64_t n, int64_t n_out) {
+  return sa.v_pos ? vrow[gs * n_out + n] : vrow[gs];
 }
 
 // forward: fold the stage into the online softmax state (m, l, num) of every position;
@@ -1303,7 +1308,7 @@ __global__ void __launch_bounds__(NT) softmax_forward_kernel(Stage st, SoftArgs 
   stage_row(X, static_cast<const T*>(st.x) + row * st.n_in, n0 + st.x_off - (int64_t)dil * half,
             span, st.n_in);
   __syncthreads();
-  const T* Vp = static_cast<const T*>(sa.v);
+  const T* vrow = v_row(sa, static_cast<const T*>(sa.v), row, st.n_out);
   constexpr T kLog = SoftExp<T>::kLog;
   const T kt = T(sa.inv_tau) * kLog;  // |W| -> |W| / tau in the exponential's base
   T mm[V], ll[V], nn[V];
@@ -1328,7 +1333,7 @@ __global__ void __launch_bounds__(NT) softmax_forward_kernel(Stage st, SoftArgs 
       for (int v = 0; v < V; ++v) {
         const int64_t n = min(n0 + tid + NT * v, st.n_out - 1);
         const T av = hw_sqrt(fma(re[v][s], re[v][s], im[v][s] * im[v][s])) * kt;
-        const T val = v_value(sa, Vp, row, gs, n, st.n_out);
+        const T val = v_value(sa, vrow, gs, n, st.n_out);
         // one exponential per value: exp(-|av - m|) rescales the state when av is the new
         // maximum and weighs av otherwise (first frequency: m = -inf, exp(-inf) = 0)
         const T dd = av - mm[v];
@@ -1376,7 +1381,7 @@ __global__ void __launch_bounds__(NT) softmax_backward_kernel(Stage st, SoftArgs
   stage_row(X, static_cast<const T*>(st.x) + row * st.n_in, n0 + st.x_off - (int64_t)dil * half,
             span, st.n_in);
   __syncthreads();
-  const T* Vp = static_cast<const T*>(sa.v);
+  const T* vrow = v_row(sa, static_cast<const T*>(sa.v), row, st.n_out);
   const T inv_tau = T(sa.inv_tau);
   constexpr T kLog = SoftExp<T>::kLog;
   const T kt = inv_tau * kLog;
@@ -1411,7 +1416,7 @@ __global__ void __launch_bounds__(NT) softmax_backward_kernel(Stage st, SoftArgs
         mag_inv(fma(rv, rv, iv * iv), mag, inv);
         const T p = SoftExp<T>::ex(fma(mag, kt, -mm[v])) * il[v];
         const T gp = ok ? gg[v] * p : T(0);
-        const T val = v_value(sa, Vp, row, gs, nc, st.n_out);
+        const T val = v_value(sa, vrow, gs, nc, st.n_out);
         const T coef = gp * (val - oo[v]) * inv_tau * inv;
         if (ok) {
           typedef T v2 __attribute__((ext_vector_type(2)));
