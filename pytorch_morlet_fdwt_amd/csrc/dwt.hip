@@ -395,8 +395,10 @@ __device__ inline void synthesis_block(const T* __restrict__ a, const T* __restr
     constexpr int H = LT / 2;
     constexpr int W = V + H - 1;
     T av[W], dv[W];
-    lds_window<(V >= 4 && sizeof(T) == 4) ? 4 : 2>(a, av);  // windows start V elements apart
-    lds_window<(V >= 4 && sizeof(T) == 4) ? 4 : 2>(d, dv);
+    // windows start V elements apart: vector reads of 4 or 2, single words for odd V
+    constexpr int WV = (V >= 4 && sizeof(T) == 4) ? 4 : (V % 2 == 0 ? 2 : 1);
+    lds_window<WV>(a, av);
+    lds_window<WV>(d, dv);
 #pragma unroll
     for (int q = 0; q < V; ++q) {
       T so = T(0), se = T(0);
@@ -1386,42 +1388,44 @@ __global__ void __launch_bounds__(NTK) synthesis_rows_kernel(SynArgs) {
     const bool vec_out = std::is_same<S, float>::value && osh == 0;
     const bool vec_shift = std::is_same<S, float>::value && osh != 0;
     const int plo = lv.plo, phi = lv.phi, pbeg = lv.pbeg, pend = lv.pend;
-    for (int vw = lv.vbeg + (tid - lane) * VR; vw < lv.vend; vw += NT * VR) {
-      const int v0 = vw + lane * VR;
-      if (v0 >= lv.vend) continue;
-      T zo[VR], ze[VR];
-      synthesis_block<T, LT, VR>(a0 + v0, dp + v0, h0, h1, L, zo, ze);
-      T v[2 * VR];
+    // VV consecutive pairs from v0 (vw: the first pair of the thread's wave, VV == VR only)
+    auto pairs = [&](auto vv, int v0, int vw) __attribute__((always_inline)) {
+      constexpr int VV = decltype(vv)::value;
+      T zo[VV], ze[VV];
+      synthesis_block<T, LT, VV>(a0 + v0, dp + v0, h0, h1, L, zo, ze);
+      T v[2 * VV];
 #pragma unroll
-      for (int q = 0; q < VR; ++q) {
+      for (int q = 0; q < VV; ++q) {
         v[2 * q] = zo[q];
         v[2 * q + 1] = ze[q];
       }
-      const int i0 = 2 * v0 + off - 1;  // first of this thread's 2 VR positions
-      if constexpr (std::is_same<S, float>::value) {
+      const int i0 = 2 * v0 + off - 1;  // first of this thread's 2 VV positions
+      if constexpr (VV == VR && std::is_same<S, float>::value) {
         // whole waves inside the plain range of the output row: shifted 16-byte stores
         const int iw = 2 * vw + off - 1;
         if (last && vec_shift && iw >= plo && iw + 128 * VR <= phi) {
           store_shifted(orow, i0, v, osh, lane);
-          continue;
+          return;
         }
       }
-      if (i0 >= plo && i0 + 2 * VR <= phi && (last ? vec_out : vec_lds)) {
-        typedef T v4 __attribute__((ext_vector_type(4)));
+      if constexpr (VV == VR) {
+        if (i0 >= plo && i0 + 2 * VR <= phi && (last ? vec_out : vec_lds)) {
+          typedef T v4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int q = 0; q < VR / 2; ++q) {
-          const v4 w = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-          if (last) {
-            if constexpr (std::is_same<S, float>::value)
-              *reinterpret_cast<v4*>(orow + i0 + 4 * q) = w;
-          } else {
-            *reinterpret_cast<v4*>(dst + i0 + 4 * q) = w;
+          for (int q = 0; q < VR / 2; ++q) {
+            const v4 w = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            if (last) {
+              if constexpr (std::is_same<S, float>::value)
+                *reinterpret_cast<v4*>(orow + i0 + 4 * q) = w;
+            } else {
+              *reinterpret_cast<v4*>(dst + i0 + 4 * q) = w;
+            }
           }
+          return;
         }
-        continue;
       }
 #pragma unroll
-      for (int j = 0; j < 2 * VR; ++j) {
+      for (int j = 0; j < 2 * VV; ++j) {
         const int p = i0 + j;
         if (p >= plo && p < phi) {
           if (last) Storage<S>::store(orow, p, v[j]);
@@ -1430,7 +1434,14 @@ __global__ void __launch_bounds__(NTK) synthesis_rows_kernel(SynArgs) {
           E[p < plo ? p - pbeg : (plo - pbeg) + (p - phi)] = v[j];
         }
       }
-    }
+    };
+    // whole passes of NT VR pairs, then the level's remainder one pair per thread: a pass
+    // costs the same with a few pairs as with all, and the remainder (a few dozen pairs on
+    // the long levels, the whole of the short ones) is on every level's critical path
+    const int vmid = lv.vbeg + (lv.vend - lv.vbeg) / (NT * VR) * (NT * VR);
+    for (int vw = lv.vbeg + (tid - lane) * VR; vw < vmid; vw += NT * VR)
+      pairs(std::integral_constant<int, VR>{}, vw + lane * VR, vw);
+    for (int v0 = vmid + tid; v0 < lv.vend; v0 += NT) pairs(std::integral_constant<int, 1>{}, v0, 0);
     __syncthreads();
 
     // fold targets near the row ends (none in zero mode); the next level's staging (other
