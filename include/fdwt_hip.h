@@ -241,6 +241,16 @@ int fdwt_softmax_backward(const void* x, const void* taps, const void* v,
                           int32_t half, const int32_t* support, const int32_t* chan,
                           int32_t dil, double inv_tau, int32_t dtype, void* stream);
 
+/* dL/dV of the per-position spectral softmax (v_per_position = 1): the backward's workspace
+ * partials part ((groups * nch) rows, n_scales, n_out), summed over each group's nch rows in
+ * row order (deterministic), are added to gv[g0 + g, chan[s], n] (gv: (v_groups, v_s_total,
+ * n_out)).  Replaces the atomic dL/dV accumulation of the reference's backward stage
+ * (src/fdwt/kernels/softmax.py:121-127, :208) for that V layout. */
+int fdwt_softmax_dv_reduce(const void* part, void* gv, int64_t groups, int32_t nch,
+                           int32_t n_scales, const int32_t* chan, int64_t v_groups,
+                           int64_t v_s_total, int64_t n_out, int64_t g0, int32_t dtype,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

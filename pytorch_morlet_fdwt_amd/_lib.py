@@ -62,6 +62,8 @@ SIGNATURES = {
     "fdwt_softmax_forward": [_P, _P, _P, _I32, _I64, _I32, _P, _P, _P, _I64, _I64, _I64, _I64,
                              _I32, _I32, _PI32, _PI32, _I32, _DBL, _I32, _I32, _I32, _P],
     "fdwt_softmax_workspace": [_I64, _I64, _I32, _I32],
+    "fdwt_softmax_dv_reduce": [_P, _P, _I64, _I32, _I32, _PI32, _I64, _I64, _I64, _I64, _I32,
+                               _P],
     "fdwt_morlet_filters": [_P, _P, _PI32, _PI32, _I32, _I32, _I32, _I32, _P, _I32, _P],
     "fdwt_morlet_filters_backward": [_P, _P, _PI32, _PI32, _I32, _I32, _I32, _I32, _P, _I32, _P,
                                      _P, _P],

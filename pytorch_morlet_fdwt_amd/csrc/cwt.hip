@@ -1463,6 +1463,31 @@ __global__ void __launch_bounds__(NT) reduce_cols_kernel(const T* __restrict__ i
   }
 }
 
+// dL/dV of the per-position spectral softmax: the backward's partials (groups nch rows,
+// n_scales, n_out) summed over each group's nch rows in row order (deterministic) and added to
+// the V gradient at the scales' global indices: grid (groups * n_scales, tiles of NT
+// positions), one position per thread, the rows' loads unrolled so several are in flight.
+struct DvArgs {
+  int32_t chan[MAXS];
+};
+template <typename T>
+__global__ void __launch_bounds__(NT) softmax_dv_kernel(const T* __restrict__ part,
+                                                        T* __restrict__ gv, DvArgs ca, int nch,
+                                                        int n_scales, int64_t v_s_total,
+                                                        int64_t n_out, int64_t g0, int tiles) {
+  const int64_t gs = blockIdx.x / tiles;  // (group, local scale)
+  const int64_t g = gs / n_scales;
+  const int s = (int)(gs % n_scales);
+  const int64_t n = (int64_t)(blockIdx.x % tiles) * NT + threadIdx.x;
+  if (n >= n_out) return;
+  const T* src = part + (g * nch * n_scales + s) * n_out + n;  // row c at c n_scales n_out
+  const int64_t rstride = (int64_t)n_scales * n_out;
+  T acc = T(0);
+#pragma unroll 8
+  for (int c = 0; c < nch; ++c) acc += src[c * rstride];
+  gv[((g0 + g) * v_s_total + ca.chan[s]) * n_out + n] += acc;
+}
+
 // ------------------------------------------------------------------ filter synthesis
 // Sampled Morlet filters (reference cwt.py:181-203): row i C + ch, column center + k,
 //   t = k dil_i / s_i,  env = exp(-t^2 / 2) [|k| <= sup_i],  amp = pi^(-1/4) dil_i / s_i^p,
@@ -2172,6 +2197,31 @@ extern "C" int64_t fdwt_softmax_workspace(int64_t rows, int64_t n_out, int32_t n
                                           int32_t v_per_position) {
   if (v_per_position) return rows * (int64_t)n_scales * n_out;
   return rows * cdiv(n_out, TT) * (int64_t)n_scales;
+}
+
+extern "C" int fdwt_softmax_dv_reduce(const void* part, void* gv, int64_t groups, int32_t nch,
+                                      int32_t n_scales, const int32_t* chan, int64_t v_groups,
+                                      int64_t v_s_total, int64_t n_out, int64_t g0,
+                                      int32_t dtype, void* stream) {
+  if (!part || !gv || !chan || groups < 0 || nch < 1 || n_scales < 0 || n_scales > MAXS ||
+      v_s_total < 1 || n_out < 0 || g0 < 0 || g0 + groups > v_groups ||
+      (dtype != FDWT_F32 && dtype != FDWT_F64))
+    return FDWT_ERR_ARG;
+  DvArgs ca{};
+  for (int s = 0; s < n_scales; ++s) {
+    if (chan[s] < 0 || chan[s] >= v_s_total) return FDWT_ERR_ARG;
+    ca.chan[s] = chan[s];
+  }
+  if (groups == 0 || n_scales == 0 || n_out == 0) return 0;
+  const int64_t tiles = cdiv(n_out, NT);
+  const int64_t blocks = groups * n_scales * tiles;
+  if (tiles > INT32_MAX || blocks > INT32_MAX) return FDWT_ERR_ARG;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (dtype == FDWT_F32)
+    return launch(softmax_dv_kernel<float>, blocks, 0, hs, (const float*)part, (float*)gv, ca,
+                  (int)nch, (int)n_scales, v_s_total, n_out, g0, (int)tiles);
+  return launch(softmax_dv_kernel<double>, blocks, 0, hs, (const double*)part, (double*)gv, ca,
+                (int)nch, (int)n_scales, v_s_total, n_out, g0, (int)tiles);
 }
 
 extern "C" int fdwt_softmax_backward(const void* x, const void* taps, const void* v,

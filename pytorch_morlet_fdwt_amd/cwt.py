@@ -641,7 +641,7 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
         nch = ctx.nch
         need_h = ctx.needs_input_grad[2]
         gH = torch.zeros_like(H) if need_h else None
-        gV = torch.zeros_like(V)
+        gV = torch.zeros_like(V, memory_format=torch.contiguous_format)
         by_oct = {st.octave: k for k, st in enumerate(plan.stages)}
         xs = _lowpass_chain(plan, x.to(dt))
         L = _lib.lib()
@@ -679,9 +679,11 @@ class _SpectralSoftmaxFunction(torch.autograd.Function):
                                     xj.shape[1], N, mj, S_g, st.half, grp.sup, grp.chan, st.dil,
                                     1.0 / ctx.tau, _lib.dtype_code(dt), _lib.stream(dev))
                         if v_pos:
-                            # (rows, S_g, N): sum the nch rows of each group
-                            part = ws[:ws_n].view(rc // nch, nch, S_g, N).sum(1)
-                            gV[r0 // nch:r1 // nch].index_add_(1, gidx, part)
+                            # (rows, S_g, N): the nch rows of each group summed (in row order)
+                            # into gV at the group's scale indices, one kernel
+                            _lib.launch("fdwt_softmax_dv_reduce", dev, _lib.ptr(ws), _lib.ptr(gV),
+                                        rc // nch, nch, S_g, grp.chan, gV.shape[0], gV.shape[1],
+                                        N, r0 // nch, _lib.dtype_code(dt), _lib.stream(dev))
                         else:
                             part = ws[:ws_n].view(rc, -1, S_g).sum(1).view(-1, nch, S_g).sum(0)
                             gV[:, gidx] += part
